@@ -1,0 +1,482 @@
+// pa_api.hip -- the extern "C" entry points of include/pagedattn.h.
+//
+// Host-side work only: argument checks (every check runs before any HIP
+// call, so a rejected call has no device side effect), the partition plan,
+// parameter packing, and kernel launches on the caller's stream.  Nothing
+// here allocates device memory; scratch comes from the caller's workspace.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "../../include/pagedattn.h"
+#include "pa_common.hpp"
+
+namespace pa {
+hipError_t launch_decode_f16(const DecodeParams& p, int gc, hipStream_t stream);
+hipError_t launch_decode_bf16(const DecodeParams& p, int gc, hipStream_t stream);
+hipError_t launch_decode_f32(const DecodeParams& p, int gc, hipStream_t stream);
+hipError_t launch_decode_f64(const DecodeParams& p, int gc, hipStream_t stream);
+
+hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int gc, hipStream_t stream) {
+  switch (kv_dtype) {
+    case kF16: return launch_decode_f16(p, gc, stream);
+    case kBF16: return launch_decode_bf16(p, gc, stream);
+    case kF32: return launch_decode_f32(p, gc, stream);
+    case kF64: return launch_decode_f64(p, gc, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+}  // namespace pa
+
+namespace {
+
+using namespace pa;
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int dtype_bytes(int dt) {
+  switch (dt) {
+    case kF32: case kI32: return 4;
+    case kF16: case kBF16: return 2;
+    case kF64: case kI64: return 8;
+    default: return 0;
+  }
+}
+
+const char* dtype_name(int dt) {
+  switch (dt) {
+    case kF32: return "float32";
+    case kF16: return "float16";
+    case kBF16: return "bfloat16";
+    case kF64: return "float64";
+    case kI32: return "int32";
+    case kI64: return "int64";
+    default: return "unknown";
+  }
+}
+
+bool is_contiguous(const pa_tensor_t* t) {
+  int64_t s = 1;
+  for (int i = t->ndim - 1; i >= 0; --i) {
+    if (t->shape[i] != 1 && t->stride[i] != s) return false;
+    s *= t->shape[i];
+  }
+  return true;
+}
+
+int64_t numel(const pa_tensor_t* t) {
+  int64_t n = 1;
+  for (int i = 0; i < t->ndim; ++i) n *= t->shape[i];
+  return n;
+}
+
+int check_tensor(const pa_tensor_t* t, const char* name, int ndim, const char* layout) {
+  if (!t) return fail(PA_ERR_INVALID_ARGUMENT, "%s is NULL", name);
+  if (t->ndim != ndim) return fail(PA_ERR_INVALID_ARGUMENT, "%s must be %s", name, layout);
+  for (int i = 0; i < ndim; ++i)
+    if (t->shape[i] < 0) return fail(PA_ERR_INVALID_ARGUMENT, "%s has a negative size", name);
+  if (!t->data && numel(t) > 0) return fail(PA_ERR_INVALID_ARGUMENT, "%s has a NULL data pointer", name);
+  return PA_OK;
+}
+
+// ------------------------------------------------------------ device info --
+
+int device_cu_count(int* cus) {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0)
+    return fail(PA_ERR_HIP, "no HIP device is available");
+  if (dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) { *cus = c; return PA_OK; }
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    return fail(PA_ERR_HIP, "cannot read the compute-unit count of device %d", dev);
+  if (dev < 64) cached[dev].store(n, std::memory_order_relaxed);
+  *cus = n;
+  return PA_OK;
+}
+
+// Tuning knobs of the partition planner, overridable for measurement sweeps.
+struct PlanKnobs {
+  int64_t wgs_per_cu = 3;   // target resident work-groups per CU
+  int64_t min_part = 256;   // shortest partition worth a work-group (tokens)
+  int64_t max_part = 2048;  // longest partition (bounds ragged imbalance)
+};
+
+const PlanKnobs& knobs() {
+  static const PlanKnobs k = [] {
+    PlanKnobs r;
+    if (const char* s = getenv("PA_PLAN_WGS_PER_CU")) r.wgs_per_cu = std::max(1L, atol(s));
+    if (const char* s = getenv("PA_PLAN_MIN_PART")) r.min_part = std::max(16L, atol(s));
+    if (const char* s = getenv("PA_PLAN_MAX_PART")) r.max_part = std::max(16L, atol(s));
+    return r;
+  }();
+  return k;
+}
+
+// ---------------------------------------------------------- decode checks --
+
+struct DecodeArgs {
+  DecodeParams p;
+  int kv_dtype;
+  int gc;
+};
+
+// Shared checks of every entry point (the TORCH_CHECKs of
+// kernels/paged_attn_v3.cu:199-216 and kernels/paged_attn_prefill.cu:128-146,
+// plus the layout rules of this ABI).  prefill selects q [B,S,H,D].
+int check_args(const pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k,
+               const pa_tensor_t* v, const pa_tensor_t* bt, const pa_tensor_t* ctx, double scale,
+               bool prefill, DecodeArgs* a) {
+  int rc;
+  const int qnd = prefill ? 4 : 3;
+  const char* qlay = prefill ? "[B, S, H, D]" : "[B, H, D]";
+  if ((rc = check_tensor(q, "q", qnd, qlay))) return rc;
+  if ((rc = check_tensor(out, "out", qnd, qlay))) return rc;
+  if ((rc = check_tensor(k, "k_cache", 4, "[NB, BS, H, D]"))) return rc;
+  if ((rc = check_tensor(v, "v_cache", 4, "[NB, BS, H, D]"))) return rc;
+  if ((rc = check_tensor(bt, "block_tables", 2, "[B, MB]"))) return rc;
+  if ((rc = check_tensor(ctx, "context_lens", 1, "[B]"))) return rc;
+
+  for (int i = 0; i < qnd; ++i)
+    if (out->shape[i] != q->shape[i])
+      return fail(PA_ERR_INVALID_ARGUMENT, "out must have the shape of q");
+  if (q->dtype != kF32 && q->dtype != kF16 && q->dtype != kBF16)
+    return fail(PA_ERR_INVALID_ARGUMENT, "q must be float32, float16 or bfloat16 (got %s)", dtype_name(q->dtype));
+  if (out->dtype != kF32 && out->dtype != kF16 && out->dtype != kBF16)
+    return fail(PA_ERR_INVALID_ARGUMENT, "out must be float32, float16 or bfloat16 (got %s)", dtype_name(out->dtype));
+  if (k->dtype != kF32 && k->dtype != kF16 && k->dtype != kBF16 && k->dtype != kF64)
+    return fail(PA_ERR_INVALID_ARGUMENT, "k_cache must be float32, float16, bfloat16 or float64 (got %s)", dtype_name(k->dtype));
+  if (v->dtype != k->dtype) return fail(PA_ERR_INVALID_ARGUMENT, "v_cache must have the dtype of k_cache");
+  if (bt->dtype != kI32) return fail(PA_ERR_INVALID_ARGUMENT, "block_tables must be int32");
+  if (ctx->dtype != kI32) return fail(PA_ERR_INVALID_ARGUMENT, "context_lens must be int32");
+  if (!is_contiguous(q)) return fail(PA_ERR_INVALID_ARGUMENT, "q must be contiguous");
+  if (!is_contiguous(out)) return fail(PA_ERR_INVALID_ARGUMENT, "out must be contiguous");
+  for (int i = 0; i < 4; ++i)
+    if (v->shape[i] != k->shape[i]) return fail(PA_ERR_INVALID_ARGUMENT, "v_cache must have the shape of k_cache");
+  if (!std::isfinite(scale)) return fail(PA_ERR_INVALID_ARGUMENT, "scale must be finite");
+
+  const int64_t B = q->shape[0];
+  const int64_t S = prefill ? q->shape[1] : 1;
+  const int64_t H = q->shape[prefill ? 2 : 1];
+  const int64_t D = q->shape[prefill ? 3 : 2];
+  const int64_t NB = k->shape[0], BS = k->shape[1], HKV = k->shape[2];
+  const int64_t MB = bt->shape[1];
+  if (bt->shape[0] != B) return fail(PA_ERR_INVALID_ARGUMENT, "block_tables must have B rows");
+  if (ctx->shape[0] != B) return fail(PA_ERR_INVALID_ARGUMENT, "context_lens must have B entries");
+  if (k->shape[3] != D) return fail(PA_ERR_INVALID_ARGUMENT, "k_cache head_dim (%lld) != q head_dim (%lld)",
+                                    (long long)k->shape[3], (long long)D);
+  if (HKV <= 0 || H <= 0 || H % HKV != 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "n_head must be divisible by n_kv_head");
+  if (BS <= 0) return fail(PA_ERR_INVALID_ARGUMENT, "block_size must be positive");
+  if (D != 32 && D != 64 && D != 128 && D != 256)
+    return fail(PA_ERR_UNSUPPORTED, "unsupported head_dim %lld", (long long)D);
+  if (k->dtype == kF64 && D > 128)
+    return fail(PA_ERR_UNSUPPORTED, "float64 KV caches support head_dim <= 128");
+  if (MB * BS >= (1LL << 31) || B * S >= (1LL << 31) || B >= (1LL << 31) || H >= (1 << 16))
+    return fail(PA_ERR_UNSUPPORTED, "problem too large for 32-bit token indices");
+  if (bt->stride[1] != 1 || (B > 1 && bt->stride[0] < MB))
+    return fail(PA_ERR_INVALID_ARGUMENT, "block_tables rows must be contiguous");
+  if (ctx->stride[0] != 1 && B > 1) return fail(PA_ERR_INVALID_ARGUMENT, "context_lens must be contiguous");
+  const int es = dtype_bytes(k->dtype);
+  for (const pa_tensor_t* t : {k, v}) {
+    if (t->stride[3] != 1)
+      return fail(PA_ERR_INVALID_ARGUMENT, "k_cache/v_cache must have a contiguous last dimension");
+    for (int i = 0; i < 3; ++i)
+      if (((t->stride[i] * es) & 15) != 0 && t->shape[i] > 1)
+        return fail(PA_ERR_UNSUPPORTED, "k_cache/v_cache strides must be multiples of 16 bytes");
+    if ((reinterpret_cast<uintptr_t>(t->data) & 15) != 0)
+      return fail(PA_ERR_UNSUPPORTED, "k_cache/v_cache must be 16-byte aligned");
+  }
+
+  DecodeParams& p = a->p;
+  memset(&p, 0, sizeof(p));
+  p.q = q->data;
+  p.out = out->data;
+  p.k = k->data;
+  p.v = v->data;
+  p.block_tables = static_cast<const int32_t*>(bt->data);
+  p.context_lens = static_cast<const int32_t*>(ctx->data);
+  p.k_sb = k->stride[0]; p.k_st = k->stride[1]; p.k_sh = k->stride[2];
+  p.v_sb = v->stride[0]; p.v_st = v->stride[1]; p.v_sh = v->stride[2];
+  p.bt_stride = B > 1 ? bt->stride[0] : MB;
+  p.num_blocks = NB;
+  p.B = (int)B; p.Sq = (int)S; p.H = (int)H; p.HKV = (int)HKV; p.G = (int)(H / HKV);
+  p.D = (int)D; p.BS = (int)BS; p.MB = (int)MB;
+  p.q_dtype = q->dtype;
+  p.out_dtype = out->dtype;
+  p.bs_div = make_fastdiv((uint32_t)BS);
+  p.qscale = (float)(scale * 1.4426950408889634);
+  a->kv_dtype = k->dtype;
+  a->gc = decode_heads_per_wg(p.G);
+  p.head_chunks = (p.G + a->gc - 1) / a->gc;
+  return PA_OK;
+}
+
+struct Plan {
+  int64_t parts;
+  int64_t part_tokens;  // 0 = reference count mode
+  bool direct;
+};
+
+int make_plan(const DecodeParams& p, int gc, int64_t num_splits, Plan* plan) {
+  if (num_splits > 0) {
+    if (num_splits > (1 << 20)) return fail(PA_ERR_INVALID_ARGUMENT, "num_splits too large");
+    plan->parts = num_splits;
+    plan->part_tokens = 0;
+    plan->direct = num_splits == 1;
+    return PA_OK;
+  }
+  int cus = 0;
+  int rc = device_cu_count(&cus);
+  if (rc) return rc;
+  int64_t ptok = 0, nparts = 0;
+  pa_plan_partitions(p.B, p.H, p.HKV, p.D, (int64_t)p.MB * p.BS, cus, &ptok, &nparts);
+  (void)gc;
+  plan->parts = nparts;
+  plan->part_tokens = nparts > 1 ? ptok : 0;
+  plan->direct = nparts <= 1;
+  return PA_OK;
+}
+
+size_t workspace_bytes_for(int64_t B, int64_t H, int64_t D, const Plan& plan) {
+  if (plan.direct) return 0;
+  const size_t rows = (size_t)B * H * plan.parts;
+  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  return up(rows * D * 4) + 2 * up(rows * 4);
+}
+
+void bind_workspace(DecodeParams* p, void* ws, const Plan& plan) {
+  const size_t rows = (size_t)p->B * p->H * plan.parts;
+  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  char* base = static_cast<char*>(ws);
+  p->ws_acc = reinterpret_cast<float*>(base);
+  p->ws_m = reinterpret_cast<float*>(base + up(rows * p->D * 4));
+  p->ws_l = reinterpret_cast<float*>(base + up(rows * p->D * 4) + up(rows * 4));
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return PA_OK;
+  return fail(PA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// One direct decode launch (one partition per sequence): v1, v2 and the
+// fp32 prefill path.
+int run_direct(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const pa_tensor_t* v,
+               const pa_tensor_t* bt, const pa_tensor_t* ctx, double scale, bool prefill,
+               void* stream) {
+  DecodeArgs a;
+  int rc = check_args(out, q, k, v, bt, ctx, scale, prefill, &a);
+  if (rc) return rc;
+  if ((int64_t)a.p.B * a.p.Sq * a.p.H == 0) return PA_OK;
+  a.p.parts = 1;
+  a.p.part_tokens = 0;
+  a.p.direct = 1;
+  return hip_status(launch_decode(a.p, a.kv_dtype, a.gc, static_cast<hipStream_t>(stream)),
+                    "decode kernel launch");
+}
+
+enum V3Phase { kBoth = 3, kPartition = 1, kReduce = 2 };
+
+int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const pa_tensor_t* v,
+           const pa_tensor_t* bt, const pa_tensor_t* ctx, double scale, int64_t num_splits,
+           void* ws, size_t ws_bytes, void* stream, int phases) {
+  DecodeArgs a;
+  int rc = check_args(out, q, k, v, bt, ctx, scale, false, &a);
+  if (rc) return rc;
+  if ((int64_t)a.p.B * a.p.H == 0) return PA_OK;
+  Plan plan;
+  if ((rc = make_plan(a.p, a.gc, num_splits, &plan))) return rc;
+  const size_t need = workspace_bytes_for(a.p.B, a.p.H, a.p.D, plan);
+  if (need > 0 && (!ws || ws_bytes < need))
+    return fail(PA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need, ws ? ws_bytes : 0);
+  if (need > 0 && (reinterpret_cast<uintptr_t>(ws) & 255) != 0)
+    return fail(PA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  a.p.parts = (int)plan.parts;
+  a.p.part_tokens = (int)plan.part_tokens;
+  a.p.direct = plan.direct ? 1 : 0;
+  if (!plan.direct) bind_workspace(&a.p, ws, plan);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (phases & kPartition) {
+    if ((rc = hip_status(launch_decode(a.p, a.kv_dtype, a.gc, s), "partition kernel launch"))) return rc;
+  }
+  if ((phases & kReduce) && !plan.direct) {
+    ReduceParams r;
+    r.out = a.p.out;
+    r.ws_acc = a.p.ws_acc;
+    r.ws_m = a.p.ws_m;
+    r.ws_l = a.p.ws_l;
+    r.context_lens = a.p.context_lens;
+    r.B = a.p.B; r.H = a.p.H; r.D = a.p.D; r.MB = a.p.MB; r.BS = a.p.BS;
+    r.out_dtype = a.p.out_dtype;
+    r.parts = a.p.parts;
+    r.part_tokens = a.p.part_tokens;
+    if ((rc = hip_status(launch_reduce(r, s), "reduce kernel launch"))) return rc;
+  }
+  return PA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pa_abi_version(void) { return PA_ABI_VERSION; }
+
+const char* pa_last_error(void) { return g_last_error.c_str(); }
+
+int64_t choose_num_splits_for(int64_t num_seqs, int64_t num_heads, int64_t max_context,
+                              int64_t num_compute_units) {
+  // kernels/paged_attn_v3.cu:170-190, compute units in place of SMs.
+  const int64_t have = std::max<int64_t>(num_seqs * num_heads, 1);
+  const int64_t by_chain = std::max<int64_t>(max_context / 32, 1);
+  const int64_t to_fill = std::max<int64_t>((num_compute_units * 8 + have - 1) / have, 1);
+  const int64_t s = std::max(by_chain, to_fill);
+  return std::max<int64_t>(1, std::min<int64_t>(s, 64));
+}
+
+int64_t choose_num_splits(int64_t num_seqs, int64_t num_heads, int64_t max_context) {
+  int cus = 0;
+  if (device_cu_count(&cus)) return -1;
+  return choose_num_splits_for(num_seqs, num_heads, max_context, cus);
+}
+
+int pa_plan_partitions(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                       int64_t max_context, int64_t num_compute_units, int64_t* partition_tokens,
+                       int64_t* num_partitions) {
+  if (!partition_tokens || !num_partitions)
+    return fail(PA_ERR_INVALID_ARGUMENT, "NULL output pointer");
+  if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads || max_context < 0 ||
+      num_compute_units <= 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "invalid planning arguments");
+  (void)head_dim;
+  const PlanKnobs& kn = knobs();
+  const int64_t G = num_heads / num_kv_heads;
+  const int64_t gc = decode_heads_per_wg((int)G);
+  const int64_t units = std::max<int64_t>(1, num_seqs * num_kv_heads * ((G + gc - 1) / gc));
+  const int64_t target = num_compute_units * kn.wgs_per_cu;
+  int64_t S = (target + units - 1) / units;                             // fill the GPU
+  S = std::max(S, (max_context + kn.max_part - 1) / kn.max_part);       // bound partition length
+  S = std::min(S, std::max<int64_t>(1, max_context / kn.min_part));     // keep partitions long
+  if (S <= 1 || max_context <= 0) {
+    *partition_tokens = std::max<int64_t>(max_context, 1);
+    *num_partitions = 1;
+    return PA_OK;
+  }
+  int64_t ptok = (max_context + S - 1) / S;
+  ptok = (ptok + 127) / 128 * 128;  // whole wave tiles for all 4 waves
+  *partition_tokens = ptok;
+  *num_partitions = (max_context + ptok - 1) / ptok;
+  if (*num_partitions <= 1) *partition_tokens = std::max<int64_t>(max_context, 1);
+  return PA_OK;
+}
+
+int paged_attention(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                    const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                    const pa_tensor_t* context_lens, double scale, void* stream) {
+  return run_direct(out, q, k_cache, v_cache, block_tables, context_lens, scale, false, stream);
+}
+
+int paged_attention_v2(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                       const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                       const pa_tensor_t* context_lens, double scale, void* stream) {
+  return run_direct(out, q, k_cache, v_cache, block_tables, context_lens, scale, false, stream);
+}
+
+int paged_attention_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                       const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                       const pa_tensor_t* context_lens, double scale, int64_t num_splits,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  return run_v3(out, q, k_cache, v_cache, block_tables, context_lens, scale, num_splits, workspace,
+                workspace_bytes, stream, kBoth);
+}
+
+int pa_v3_partition(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                    const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                    const pa_tensor_t* context_lens, double scale, int64_t num_splits,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  return run_v3(out, q, k_cache, v_cache, block_tables, context_lens, scale, num_splits, workspace,
+                workspace_bytes, stream, kPartition);
+}
+
+int pa_v3_reduce(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                 const pa_tensor_t* block_tables, const pa_tensor_t* context_lens,
+                 int64_t num_splits, void* workspace, size_t workspace_bytes, void* stream) {
+  return run_v3(out, q, k_cache, k_cache, block_tables, context_lens, 1.0, num_splits, workspace,
+                workspace_bytes, stream, kReduce);
+}
+
+size_t paged_attention_v3_workspace_size(const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                                         const pa_tensor_t* block_tables, int64_t num_splits) {
+  if (check_tensor(q, "q", 3, "[B, H, D]") || check_tensor(k_cache, "k_cache", 4, "[NB, BS, H, D]") ||
+      check_tensor(block_tables, "block_tables", 2, "[B, MB]"))
+    return (size_t)-1;
+  const int64_t B = q->shape[0], H = q->shape[1], D = q->shape[2];
+  const int64_t BS = k_cache->shape[1], HKV = k_cache->shape[2], MB = block_tables->shape[1];
+  if (HKV <= 0 || H % HKV) {
+    fail(PA_ERR_INVALID_ARGUMENT, "n_head must be divisible by n_kv_head");
+    return (size_t)-1;
+  }
+  DecodeParams p;
+  memset(&p, 0, sizeof(p));
+  p.B = (int)B; p.H = (int)H; p.HKV = (int)HKV; p.D = (int)D; p.BS = (int)BS; p.MB = (int)MB;
+  Plan plan;
+  if (make_plan(p, decode_heads_per_wg((int)(H / HKV)), num_splits, &plan)) return (size_t)-1;
+  return workspace_bytes_for(B, H, D, plan);
+}
+
+int paged_attention_prefill(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                            const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                            const pa_tensor_t* context_lens, double scale, void* stream) {
+  return run_direct(out, q, k_cache, v_cache, block_tables, context_lens, scale, true, stream);
+}
+
+int paged_attention_prefill_wmma(pa_tensor_t* out, const pa_tensor_t* q,
+                                 const pa_tensor_t* k_cache, const pa_tensor_t* v_cache,
+                                 const pa_tensor_t* block_tables,
+                                 const pa_tensor_t* context_lens, double scale, void* stream) {
+  DecodeArgs a;
+  int rc = check_args(out, q, k_cache, v_cache, block_tables, context_lens, scale, true, &a);
+  if (rc) return rc;
+  // kernels/paged_attn_wmma.cu:220-223 requires fp16; bf16 is served as well.
+  if (a.kv_dtype != kF16 && a.kv_dtype != kBF16)
+    return fail(PA_ERR_INVALID_ARGUMENT, "the MFMA path needs an fp16 or bf16 KV cache");
+  if (a.p.D > 256) return fail(PA_ERR_UNSUPPORTED, "unsupported head_dim for the MFMA path: %d", a.p.D);
+  if ((int64_t)a.p.B * a.p.Sq * a.p.H == 0) return PA_OK;
+  PrefillParams pp;
+  memset(&pp, 0, sizeof(pp));
+  const DecodeParams& p = a.p;
+  pp.q = p.q; pp.out = p.out; pp.k = p.k; pp.v = p.v;
+  pp.block_tables = p.block_tables; pp.context_lens = p.context_lens;
+  pp.k_sb = p.k_sb; pp.k_st = p.k_st; pp.k_sh = p.k_sh;
+  pp.v_sb = p.v_sb; pp.v_st = p.v_st; pp.v_sh = p.v_sh;
+  pp.bt_stride = p.bt_stride; pp.num_blocks = p.num_blocks;
+  pp.B = p.B; pp.S = p.Sq; pp.H = p.H; pp.HKV = p.HKV; pp.G = p.G; pp.D = p.D; pp.BS = p.BS; pp.MB = p.MB;
+  pp.q_dtype = p.q_dtype; pp.out_dtype = p.out_dtype;
+  pp.q_tiles = (p.Sq + 63) / 64;
+  pp.q_split = p.q_dtype != a.kv_dtype;
+  pp.bs_div = p.bs_div;
+  pp.qscale = p.qscale;
+  return hip_status(launch_prefill_mfma(pp, a.kv_dtype, static_cast<hipStream_t>(stream)),
+                    "prefill kernel launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,114 @@
+// pa_common.hpp -- types shared by the host launchers and the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pa {
+
+enum Dtype : int32_t { kF32 = 0, kF16 = 1, kBF16 = 2, kF64 = 3, kI32 = 4, kI64 = 5 };
+
+constexpr float kNegBig = -3.0e38f;          // empty-softmax sentinel (kernels/paged_attn_v3.cu:21)
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Unsigned division by a runtime constant d (1 <= d < 2^31) for n < 2^31:
+// q = (umulhi(n, m) + n) >> s with s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1
+// (Granlund & Montgomery, "Division by invariant integers using multiplication", 1994).
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  f.d = d;
+  f.s = 0;
+  while ((1ull << f.s) < d) ++f.s;
+  f.m = (uint32_t)(((1ull << 32) * ((1ull << f.s) - d)) / d + 1);
+  return f;
+}
+
+__host__ __device__ inline uint32_t fastdiv(uint32_t n, const FastDiv& f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t hi = __umulhi(n, f.m);
+#else
+  const uint32_t hi = (uint32_t)(((uint64_t)n * f.m) >> 32);
+#endif
+  return (hi + n) >> f.s;
+}
+
+// Everything one decode launch needs.  q/out are [Bq, Sq, H, D] contiguous;
+// decode has Sq = 1.  For the fp32 prefill path every query row is its own
+// decode problem with context ctx_b - Sq + s + 1 (kernels/paged_attn_prefill.cu:62-65).
+struct DecodeParams {
+  const void* q;
+  void* out;
+  const void* k;
+  const void* v;
+  const int32_t* block_tables;
+  const int32_t* context_lens;
+  float* ws_acc;  // [B][H][parts][D]
+  float* ws_m;    // [B][H][parts]
+  float* ws_l;    // [B][H][parts]
+  int64_t k_sb, k_st, k_sh;  // element strides of k_cache: block, token, head
+  int64_t v_sb, v_st, v_sh;
+  int64_t bt_stride;   // elements between block-table rows
+  int64_t num_blocks;  // NB: valid block ids are [0, NB)
+  int32_t B, Sq, H, HKV, G, D, BS, MB;
+  int32_t head_chunks;  // ceil(G / GC): WGs per KV head
+  int32_t q_dtype, out_dtype;
+  int32_t parts;        // partitions per (sequence, KV head) in the grid
+  int32_t part_tokens;  // > 0: fixed partition length; 0: chunk = ceil(ctx / parts)
+  int32_t direct;       // 1: one partition, every WG writes the normalised output
+  FastDiv bs_div;
+  float qscale;         // scale * log2(e): scores come out in log2 units
+};
+
+struct ReduceParams {
+  void* out;
+  const float* ws_acc;
+  const float* ws_m;
+  const float* ws_l;
+  const int32_t* context_lens;
+  int32_t B, H, D, MB, BS;
+  int32_t out_dtype;
+  int32_t parts;
+  int32_t part_tokens;
+};
+
+struct PrefillParams {
+  const void* q;   // [B, S, H, D]
+  void* out;       // [B, S, H, D]
+  const void* k;
+  const void* v;
+  const int32_t* block_tables;
+  const int32_t* context_lens;
+  int64_t k_sb, k_st, k_sh;
+  int64_t v_sb, v_st, v_sh;
+  int64_t bt_stride;
+  int64_t num_blocks;
+  int32_t B, S, H, HKV, G, D, BS, MB;
+  int32_t q_dtype, out_dtype;
+  int32_t q_tiles;   // ceil(S / QBLOCK)
+  int32_t q_split;   // q is not exactly the KV type: add a low-part product
+  FastDiv bs_div;
+  float qscale;      // scale * log2(e)
+};
+
+// Host launchers (defined in the kernel translation units).
+hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int gc, hipStream_t stream);
+hipError_t launch_reduce(const ReduceParams& p, hipStream_t stream);
+hipError_t launch_prefill_mfma(const PrefillParams& p, int kv_dtype, hipStream_t stream);
+
+// Heads per decode work-group for a GQA group of G query heads.
+inline int decode_heads_per_wg(int G) {
+  if (G <= 1) return 1;
+  if (G <= 2) return 2;
+  if (G <= 4) return 4;
+  if (G <= 8) return 8;
+  if (G % 8 == 0) return 8;
+  if (G % 4 == 0) return 4;
+  if (G % 2 == 0) return 2;
+  return 1;
+}
+
+}  // namespace pa

@@ -1,0 +1,9 @@
+// Decode kernels for f16 K/V caches (instantiated per KV type so the
+// translation units build in parallel).
+#include "pa_decode.hpp"
+
+namespace pa {
+hipError_t launch_decode_f16(const DecodeParams& p, int gc, hipStream_t stream) {
+  return launch_decode_kv<KvF16>(p, gc, stream);
+}
+}  // namespace pa

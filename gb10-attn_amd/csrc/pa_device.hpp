@@ -1,0 +1,127 @@
+// pa_device.hpp -- device helpers for the gfx950 kernels: KV element codecs,
+// DPP lane reductions, dtype-generic loads/stores.
+#pragma once
+
+#include "pa_common.hpp"
+
+namespace pa {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- KV types --
+// Each KV storage type is read 16 bytes per lane (one global_load_dwordx4)
+// and widened to fp32 in registers.
+
+struct KvF16 {
+  static constexpr int kBytes = 2;
+  static constexpr int kVec = 8;
+  static constexpr int kCode = kF16;
+  __device__ static inline void widen(const u32x4_t& r, float (&o)[kVec]) {
+    const half8_t h = __builtin_bit_cast(half8_t, r);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (float)h[e];
+  }
+};
+
+struct KvBF16 {
+  static constexpr int kBytes = 2;
+  static constexpr int kVec = 8;
+  static constexpr int kCode = kBF16;
+  __device__ static inline void widen(const u32x4_t& r, float (&o)[kVec]) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      o[2 * w] = __builtin_bit_cast(float, r[w] << 16);
+      o[2 * w + 1] = __builtin_bit_cast(float, r[w] & 0xffff0000u);
+    }
+  }
+};
+
+struct KvF32 {
+  static constexpr int kBytes = 4;
+  static constexpr int kVec = 4;
+  static constexpr int kCode = kF32;
+  __device__ static inline void widen(const u32x4_t& r, float (&o)[kVec]) {
+    // Cast the whole vector: bit-casting single vector elements miscompiles
+    // to one dword load reused for every element.
+    const float4_t f = __builtin_bit_cast(float4_t, r);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = f[e];
+  }
+};
+
+struct KvF64 {
+  static constexpr int kBytes = 8;
+  static constexpr int kVec = 2;
+  static constexpr int kCode = kF64;
+  __device__ static inline void widen(const u32x4_t& r, float (&o)[kVec]) {
+    const uint64_t a = ((uint64_t)r[1] << 32) | r[0];
+    const uint64_t b = ((uint64_t)r[3] << 32) | r[2];
+    o[0] = (float)__builtin_bit_cast(double, a);
+    o[1] = (float)__builtin_bit_cast(double, b);
+  }
+};
+
+__device__ inline u32x4_t load16(const void* base, int64_t byte_off) {
+  return *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+
+// ------------------------------------------------------- scalar element I/O --
+
+__device__ inline float load_elem(const void* p, int dtype, int64_t i) {
+  switch (dtype) {
+    case kF16: return (float)reinterpret_cast<const _Float16*>(p)[i];
+    case kBF16:
+      return __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(p)[i] << 16);
+    case kF64: return (float)reinterpret_cast<const double*>(p)[i];
+    default: return reinterpret_cast<const float*>(p)[i];
+  }
+}
+
+// fp32 -> bf16 with round-to-nearest-even (NaN kept quiet).
+__device__ inline uint16_t f32_to_bf16_bits(float x) {
+  uint32_t u = __builtin_bit_cast(uint32_t, x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ inline void store_elem(void* p, int dtype, int64_t i, float x) {
+  switch (dtype) {
+    case kF16: reinterpret_cast<_Float16*>(p)[i] = (_Float16)x; break;
+    case kBF16: reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(x); break;
+    default: reinterpret_cast<float*>(p)[i] = x; break;
+  }
+}
+
+// ------------------------------------------------------- lane reductions --
+// DPP row operations stay inside 16-lane rows and need no LDS traffic.
+
+template <int CTRL>
+__device__ inline float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i inside each 8-lane half row
+constexpr int kDppMirror = 0x140;     // lane i <-> 15-i inside each 16-lane row
+
+// Sum over aligned groups of N consecutive lanes (N a power of two <= 64);
+// every lane of a group receives the group's total.
+template <int N>
+__device__ inline float group_sum(float v) {
+  if constexpr (N >= 2) v += dpp<kDppXor1>(v);
+  if constexpr (N >= 4) v += dpp<kDppXor2>(v);
+  if constexpr (N >= 8) v += dpp<kDppHalfMirror>(v);
+  if constexpr (N >= 16) v += dpp<kDppMirror>(v);
+  if constexpr (N >= 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (N >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace pa

@@ -1,0 +1,178 @@
+/*
+ * pagedattn.h -- C-ABI of the MI355X (gfx950) paged-attention library.
+ *
+ * Drop-in boundary for the reference's torch::Tensor launchers declared in
+ * kernels/paged_attn_v1.h, kernels/paged_attn_v2.h, kernels/paged_attn_v3.h,
+ * kernels/paged_attn_prefill.h and kernels/paged_attn_wmma.h (gb10-attn).
+ *
+ * Every reference launcher takes (q, k_cache, v_cache, block_tables,
+ * context_lens, scale[, num_splits]) and returns a freshly allocated fp32
+ * tensor.  A C ABI cannot return a tensor, so here:
+ *   - each tensor argument is a pa_tensor_t view (device pointer, dtype,
+ *     shape, element strides) -- plain C, no torch types;
+ *   - the output is a caller-allocated pa_tensor_t (fp32 as in the reference,
+ *     or fp16/bf16);
+ *   - scratch for the context split is a caller-provided workspace whose size
+ *     is queried with paged_attention_v3_workspace_size();
+ *   - work is enqueued asynchronously on the given HIP stream (hipStream_t,
+ *     NULL = the null stream, which is where the reference launches);
+ *   - the return value is a pa_status_t; on failure pa_last_error() returns a
+ *     thread-local message.  Every argument check runs on the host before any
+ *     HIP call, so a rejected call touches no device state.
+ *
+ * Layouts (the reference's, kernels/paged_attn_v3.cu:51-55):
+ *   decode q / out      [B, H, D]
+ *   prefill q / out     [B, S, H, D]
+ *   k_cache / v_cache   [NB, BS, HKV, D]   (any element strides; the last dim
+ *                                           must be contiguous; all offsets are
+ *                                           computed in 64 bits)
+ *   block_tables        int32 [B, MB]      (row stride may exceed MB)
+ *   context_lens        int32 [B]
+ * Token j of sequence b, KV head kvh, lives at
+ *   k_cache[block_tables[b][j / BS], j % BS, kvh, :]
+ * and query head h reads KV head h / (H / HKV) (kernels/paged_attn_v3.cu:63,87-89).
+ *
+ * Behaviour the reference leaves undefined, fixed here:
+ *   - context_lens[b] <= 0: the output rows of sequence b are written as zeros
+ *     (reference: v1/v2 leave garbage, v3 writes NaN);
+ *   - context_lens[b] > MB*BS, or a block id outside [0, NB) on the sequence's
+ *     live pages: the output rows of that sequence are NaN and no out-of-range
+ *     memory is read (reference: out-of-bounds reads).
+ */
+#ifndef PAGEDATTN_H_
+#define PAGEDATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PA_ABI_VERSION 1
+#define PA_MAX_DIMS 4
+
+typedef enum pa_dtype {
+  PA_DTYPE_F32 = 0,
+  PA_DTYPE_F16 = 1,
+  PA_DTYPE_BF16 = 2,
+  PA_DTYPE_F64 = 3,
+  PA_DTYPE_I32 = 4,
+  PA_DTYPE_I64 = 5
+} pa_dtype_t;
+
+typedef enum pa_status {
+  PA_OK = 0,
+  PA_ERR_INVALID_ARGUMENT = 1, /* shape / dtype / null-pointer errors (TORCH_CHECK in the reference) */
+  PA_ERR_UNSUPPORTED = 2,      /* valid request this build does not serve (e.g. head_dim 96) */
+  PA_ERR_WORKSPACE = 3,        /* workspace missing or too small */
+  PA_ERR_HIP = 4               /* a HIP runtime call or kernel launch failed */
+} pa_status_t;
+
+/* A strided view of device memory, the C counterpart of a torch::Tensor argument. */
+typedef struct pa_tensor {
+  void* data;                   /* device pointer to element [0, ..., 0] */
+  int32_t dtype;                /* pa_dtype_t */
+  int32_t ndim;                 /* 1..PA_MAX_DIMS */
+  int64_t shape[PA_MAX_DIMS];
+  int64_t stride[PA_MAX_DIMS];  /* in elements, not bytes */
+} pa_tensor_t;
+
+/* ABI version this library was built with (PA_ABI_VERSION). */
+int pa_abi_version(void);
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* pa_last_error(void);
+
+/* Decode, naive-fused semantics.  Replaces paged_attention(),
+ * kernels/paged_attn_v1.h:13-15 (kernels/paged_attn_v1.cu:112-159).
+ * q [B,H,D] f32|f16|bf16; k/v [NB,BS,HKV,D] f32|f16|bf16|f64; out [B,H,D] f32|f16|bf16. */
+int paged_attention(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                    const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                    const pa_tensor_t* context_lens, double scale, void* stream);
+
+/* Decode, online-softmax semantics.  Replaces paged_attention_v2(),
+ * kernels/paged_attn_v2.h:13-15 (kernels/paged_attn_v2.cu:124-177). */
+int paged_attention_v2(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                       const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                       const pa_tensor_t* context_lens, double scale, void* stream);
+
+/* Decode with a FlashDecoding context split followed by a separate
+ * log-sum-exp reduce kernel.  Replaces paged_attention_v3(),
+ * kernels/paged_attn_v3.h:13-16 (kernels/paged_attn_v3.cu:192-261).
+ * num_splits > 0: sequence b is cut into num_splits partitions
+ *   [s*chunk, min((s+1)*chunk, ctx_b)), chunk = ceil(ctx_b / num_splits),
+ *   exactly as kernels/paged_attn_v3.cu:65-68.
+ * num_splits <= 0: the library plans fixed-size partitions from MB*BS, the
+ *   batch size and the device's CU count (see pa_plan_partitions); when the
+ *   batch alone fills the GPU no split and no reduce launch happen.
+ * workspace must be device memory of at least
+ *   paged_attention_v3_workspace_size(...) bytes (NULL allowed when that is 0). */
+int paged_attention_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                       const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                       const pa_tensor_t* context_lens, double scale, int64_t num_splits,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes paged_attention_v3 needs for these arguments on the current
+ * device (0 when no split is planned).  Returns (size_t)-1 on invalid arguments. */
+size_t paged_attention_v3_workspace_size(const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                                         const pa_tensor_t* block_tables, int64_t num_splits);
+
+/* The two launches paged_attention_v3 makes, exported for callers that time
+ * or interleave them.  pa_v3_partition writes per-partition softmax state
+ * into the workspace (or, for sequences that fit one partition, the final
+ * output); pa_v3_reduce merges it.  Calling both back to back on one stream
+ * is exactly paged_attention_v3.
+ * Workspace layout for a plan with P partitions per sequence:
+ *   float acc[B][H][P][D]   un-normalised sum_j p_j v_j   (kernels/paged_attn_v3.cu:113-122)
+ *   float m  [B][H][P]      running max, in log2 units (score * scale * log2 e)
+ *   float l  [B][H][P]      sum_j p_j
+ * An empty partition has m = -3e38 and l = 0 (kernels/paged_attn_v3.cu:76-77). */
+int pa_v3_partition(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                    const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                    const pa_tensor_t* context_lens, double scale, int64_t num_splits,
+                    void* workspace, size_t workspace_bytes, void* stream);
+int pa_v3_reduce(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                 const pa_tensor_t* block_tables, const pa_tensor_t* context_lens,
+                 int64_t num_splits, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Split count of the reference heuristic, kernels/paged_attn_v3.cu:170-190:
+ *   clamp(max(max_context / 32, ceil(8 * CUs / (num_seqs * num_heads))), 1, 64)
+ * with the current device's compute-unit count in place of the SM count.
+ * Returns -1 (and sets pa_last_error) when no device can be queried. */
+int64_t choose_num_splits(int64_t num_seqs, int64_t num_heads, int64_t max_context);
+
+/* The same formula for an explicit compute-unit count; pure, needs no GPU. */
+int64_t choose_num_splits_for(int64_t num_seqs, int64_t num_heads, int64_t max_context,
+                              int64_t num_compute_units);
+
+/* The partition plan paged_attention_v3 uses when num_splits <= 0, for an
+ * explicit CU count; pure, needs no GPU.  Writes the partition length in
+ * tokens and the number of partitions per sequence (1 = no split). */
+int pa_plan_partitions(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads,
+                       int64_t head_dim, int64_t max_context, int64_t num_compute_units,
+                       int64_t* partition_tokens, int64_t* num_partitions);
+
+/* Causal (chunked) prefill, fp32 arithmetic.  Replaces paged_attention_prefill(),
+ * kernels/paged_attn_prefill.h:13-15 (kernels/paged_attn_prefill.cu:122-175).
+ * Query s of sequence b sits at q_pos = ctx_b - S + s and attends keys
+ * [0, q_pos]; q_pos < 0 gives a zero row (kernels/paged_attn_prefill.cu:62-74). */
+int paged_attention_prefill(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                            const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                            const pa_tensor_t* context_lens, double scale, void* stream);
+
+/* Causal (chunked) prefill on CDNA4 matrix cores.  Replaces
+ * paged_attention_prefill_wmma(), kernels/paged_attn_wmma.h:13-15
+ * (kernels/paged_attn_wmma.cu:212-274).  K/V fp16 (as the reference) or
+ * bf16; Q and the probabilities are rounded to the KV type before each
+ * matrix product, accumulation is fp32.  D in {32, 64, 128}. */
+int paged_attention_prefill_wmma(pa_tensor_t* out, const pa_tensor_t* q,
+                                 const pa_tensor_t* k_cache, const pa_tensor_t* v_cache,
+                                 const pa_tensor_t* block_tables,
+                                 const pa_tensor_t* context_lens, double scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGEDATTN_H_ */

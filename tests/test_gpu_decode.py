@@ -1,0 +1,294 @@
+"""GPU parity of the decode entry points (paged_attention, _v2, _v3) against the CPU oracle.
+
+Inputs are seeded on the host; the oracle and the HIP kernels read the same
+buffers.  Bar: max-abs 2e-3 / rel 1e-2 for fp16/bf16 data (north star),
+1e-4 for fp32 data; block-table gather and partition indexing bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _helpers import ATOL32, RTOL32, close, decode_case, dev_inputs, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+ENTRIES = ["v1", "v2", "v3auto", "v3s1", "v3s2", "v3s7", "v3s64"]
+
+
+def run(pa, entry, q, k, v, bt, ctx, scale, **kw):
+    if entry == "v1":
+        return pa.paged_attention(q, k, v, bt, ctx, scale, **kw)
+    if entry == "v2":
+        return pa.paged_attention_v2(q, k, v, bt, ctx, scale, **kw)
+    ns = 0 if entry == "v3auto" else int(entry[3:])
+    return pa.paged_attention_v3(q, k, v, bt, ctx, scale, ns, **kw)
+
+
+def want_of(inp, scale):
+    return oracle.decode(inp["q_f32"], inp["k"], inp["v"], inp["bt"], inp["ctx"], scale, inp["kv"])
+
+
+@pytest.mark.parametrize("entry", ENTRIES)
+def test_config1_gpt2_fp16(pa, dev, entry):
+    """H=12, D=64, BS=16, B=4, ctx=512, fp16 Q/K/V, fp16 out,
+    128 physical blocks, block table a seeded permutation."""
+    inp = decode_case(4, 12, 12, 64, 16, [512] * 4, seed=11, kv="f16", q="f16")
+    assert inp["NB"] == 128
+    scale = 1.0 / np.sqrt(64)
+    got = run(pa, entry, *dev_inputs(inp, dev), scale, out_dtype=torch.float16)
+    close(to_host(got), want_of(inp, scale))
+
+
+@pytest.mark.parametrize("entry", ENTRIES)
+def test_hip_selftest_shape_fp32(pa, dev, entry):
+    """rocm/hip/paged_attn_v1_hip.cpp:151-162 shape (B=2 H=4 HKV=2 D=32 BS=16 MB=4
+    NB=8 ctx=48, U(-0.25,0.25)) against the committed golden output of the
+    reference's own cpu_reference."""
+    g = np.load(oracle.HERE.parent / "tests" / "golden" / "hip_selftest.npz")
+    q = torch.from_numpy(g["q"]).to(dev)
+    k = torch.from_numpy(g["k"]).to(dev)
+    v = torch.from_numpy(g["v"]).to(dev)
+    bt = torch.from_numpy(g["bt"]).to(dev)
+    ctx = torch.from_numpy(g["ctx"]).to(dev)
+    got = run(pa, entry, q, k, v, bt, ctx, float(g["scale"]))
+    close(to_host(got), g["out"], atol=3e-6, rtol=1e-5)
+
+
+@pytest.mark.parametrize("kv", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("G", [1, 4])
+def test_dtype_dim_gqa_matrix(pa, dev, kv, D, G):
+    HKV = 2
+    ctx = [1, 15, 16, 17, 333, 1000]
+    inp = decode_case(len(ctx), HKV * G, HKV, D, 16, ctx, seed=D * 10 + G, kv=kv)
+    scale = 1.0 / np.sqrt(D)
+    want = want_of(inp, scale)
+    tol = dict(atol=ATOL32, rtol=RTOL32) if kv == "f32" else {}
+    for entry in ("v2", "v3auto", "v3s7"):
+        got = run(pa, entry, *dev_inputs(inp, dev), scale)
+        close(to_host(got), want, **tol)
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_fp64_cache(pa, dev, D):
+    inp = decode_case(3, 8, 4, D, 16, [5, 64, 200], seed=3, kv="f64")
+    scale = 0.3
+    got = run(pa, "v3s2", *dev_inputs(inp, dev), scale)
+    close(to_host(got), want_of(inp, scale), atol=ATOL32, rtol=RTOL32)
+
+
+@pytest.mark.parametrize("G", [1, 2, 3, 4, 5, 6, 8, 12, 16, 32])
+def test_gqa_groups(pa, dev, G):
+    HKV = 2 if G <= 8 else 1
+    inp = decode_case(3, HKV * G, HKV, 128, 16, [77, 513, 2000], seed=G, kv="bf16", q="bf16")
+    scale = 1.0 / np.sqrt(128)
+    want = want_of(inp, scale)
+    for entry in ("v1", "v3auto", "v3s3"):
+        got = run(pa, entry, *dev_inputs(inp, dev), scale, out_dtype=torch.bfloat16)
+        close(to_host(got), want)
+
+
+@pytest.mark.parametrize("BS", [1, 5, 8, 32, 64])
+def test_block_sizes(pa, dev, BS):
+    ctx = [1, BS, BS + 1, 3 * BS + 2, 300]
+    inp = decode_case(len(ctx), 4, 4, 64, BS, ctx, seed=BS, kv="f16")
+    scale = 0.125
+    want = want_of(inp, scale)
+    for entry in ENTRIES:
+        close(to_host(run(pa, entry, *dev_inputs(inp, dev), scale)), want)
+
+
+@pytest.mark.parametrize("qt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("ot", [torch.float32, torch.float16, torch.bfloat16])
+def test_q_and_out_dtypes(pa, dev, qt, ot):
+    inp = decode_case(2, 8, 2, 64, 16, [100, 257], seed=5, kv="f16", q=qt)
+    got = run(pa, "v3s4", *dev_inputs(inp, dev), 0.125, out_dtype=ot)
+    assert got.dtype == ot
+    close(to_host(got), want_of(inp, 0.125))
+
+
+@pytest.mark.parametrize("entry", ENTRIES)
+def test_edge_contexts(pa, dev, entry):
+    """ctx 0 -> zero rows; ctx beyond MB*BS -> NaN rows; both without any read past the table."""
+    inp = decode_case(4, 4, 4, 64, 16, [0, 40, 33, 7], seed=9, kv="f16", mb=3)
+    ctx = inp["ctx"].copy()
+    ctx[2] = 49  # > MB*BS = 48
+    q, k, v, bt, _ = dev_inputs(inp, dev)
+    got = to_host(run(pa, entry, q, k, v, bt, torch.from_numpy(ctx).to(dev), 0.125))
+    assert np.all(got[0] == 0.0)
+    assert np.all(np.isnan(got[2]))
+    want = oracle.decode(inp["q_f32"], inp["k"], inp["v"], inp["bt"], ctx, 0.125, "f16")
+    close(got[[1, 3]], want[[1, 3]])
+
+
+@pytest.mark.parametrize("entry", ENTRIES)
+def test_bad_block_id_poisons_row(pa, dev, entry):
+    inp = decode_case(3, 4, 2, 64, 16, [40, 40, 40], seed=4, kv="f16")
+    bt = inp["bt"].copy()
+    bt[1, 1] = inp["NB"] + 5  # outside [0, NB)
+    bt[2, 2] = -1
+    q, k, v, _, ctx = dev_inputs(inp, dev)
+    got = to_host(run(pa, entry, q, k, v, torch.from_numpy(bt).to(dev), ctx, 0.125))
+    assert np.all(np.isnan(got[1])) and np.all(np.isnan(got[2]))
+    want = want_of(inp, 0.125)
+    close(got[0], want[0])
+
+
+def test_gather_bit_exact_planted_keys(pa, dev):
+    """Each (b, h) gets one dominant key (score ~ +1e4 above the rest), so
+    softmax is exactly one-hot and out must equal that token's V row bit for
+    bit: proves the block-table gather of every planted position."""
+    B, H, D, BS = 4, 4, 64, 16
+    ctx = [123, 256, 31, 400]
+    rng = np.random.default_rng(0)
+    inp = decode_case(B, H, H, D, BS, ctx, seed=21, kv="f32", q="f32")
+    k = np.zeros_like(inp["k"])
+    q = np.zeros((B, H, D), np.float32)
+    for trial in range(3):
+        pos = np.zeros((B, H), np.int64)
+        for b in range(B):
+            for h in range(H):
+                j = int(rng.integers(0, ctx[b]))
+                pos[b, h] = j
+                blk, off = inp["bt"][b, j // BS], j % BS
+                k[blk, off, h, :] = 0.0
+                k[blk, off, h, h] = 100.0
+                q[b, h, :] = 0.0
+                q[b, h, h] = 1000.0
+        qd = torch.from_numpy(q).to(dev)
+        kd = torch.from_numpy(k).to(dev)
+        vd = torch.from_numpy(inp["v"]).to(dev)
+        bt = torch.from_numpy(inp["bt"]).to(dev)
+        cd = torch.from_numpy(inp["ctx"]).to(dev)
+        for entry in ENTRIES:
+            got = to_host(run(pa, entry, qd, kd, vd, bt, cd, 1.0))
+            for b in range(B):
+                for h in range(H):
+                    j = pos[b, h]
+                    row = inp["v"][inp["bt"][b, j // BS], j % BS, h, :]
+                    assert np.array_equal(got[b, h], row), (entry, b, h, j)
+        for b in range(B):
+            for h in range(H):
+                j = pos[b, h]
+                k[inp["bt"][b, j // BS], j % BS, h, :] = 0.0
+
+
+def test_block_permutation_invariance_bit_exact(pa, dev):
+    """Moving physical blocks and rewriting the table identically must not change a bit."""
+    inp = decode_case(3, 8, 2, 128, 16, [300, 64, 511], seed=8, kv="bf16", extra_blocks=7)
+    perm = np.random.default_rng(1).permutation(inp["NB"])
+    k2 = np.empty_like(inp["k"])
+    v2 = np.empty_like(inp["v"])
+    k2[perm] = inp["k"]
+    v2[perm] = inp["v"]
+    bt2 = perm[inp["bt"]].astype(np.int32)
+    q, k, v, bt, ctx = dev_inputs(inp, dev)
+    for entry in ENTRIES:
+        a = to_host(run(pa, entry, q, k, v, bt, ctx, 0.1))
+        b = to_host(run(pa, entry, q, to_dev(k2, "bf16", dev), to_dev(v2, "bf16", dev),
+                        torch.from_numpy(bt2).to(dev), ctx, 0.1))
+        assert np.array_equal(a, b), entry
+
+
+def test_repeat_calls_bit_identical(pa, dev):
+    inp = decode_case(5, 12, 12, 64, 16, [2048, 1, 700, 1500, 64], seed=2, kv="f16")
+    args = dev_inputs(inp, dev)
+    for entry in ("v2", "v3auto", "v3s64"):
+        a = to_host(run(pa, entry, *args, 0.125))
+        for _ in range(3):
+            assert np.array_equal(a, to_host(run(pa, entry, *args, 0.125)))
+
+
+def test_strided_layer_view_of_pool(pa, dev):
+    """K/V passed as one layer of a [L, 2, NB, BS, HKV, D] pool (no copy)."""
+    L, NB, BS, HKV, D = 3, 40, 16, 4, 64
+    rng = np.random.default_rng(6)
+    pool = rng.standard_normal((L, 2, NB, BS, HKV, D), dtype=np.float32).astype(np.float16)
+    inp = decode_case(2, 8, HKV, D, BS, [200, 311], seed=6, kv="f16", extra_blocks=NB - 33)
+    assert inp["NB"] == NB
+    layer = 2
+    pd = torch.from_numpy(pool).to(dev)
+    q, _, _, bt, ctx = dev_inputs(inp, dev)
+    kd, vd = pd[layer, 0], pd[layer, 1]
+    want = oracle.decode(inp["q_f32"], pool[layer, 0], pool[layer, 1], inp["bt"], inp["ctx"], 0.125, "f16")
+    for entry in ENTRIES:
+        close(to_host(run(pa, entry, q, kd, vd, bt, ctx, 0.125)), want)
+    # Block-major pool [NB, L, 2, BS, HKV, D]: block stride L*2*BS*HKV*D elements.
+    pool2 = np.ascontiguousarray(np.transpose(pool, (2, 0, 1, 3, 4, 5)))
+    p2 = torch.from_numpy(pool2).to(dev)
+    for entry in ENTRIES:
+        close(to_host(run(pa, entry, q, p2[:, layer, 0], p2[:, layer, 1], bt, ctx, 0.125)), want)
+
+
+def test_partition_bounds_bit_exact(pa, dev):
+    """With K = 0 every score is 0, so each partition's l is exactly its token
+    count: the kernel's partitions must be [s*chunk, min((s+1)*chunk, ctx)),
+    chunk = ceil(ctx/S) (kernels/paged_attn_v3.cu:65-68), empty ones m=-3e38, l=0."""
+    import ctypes as C
+    ctx = [1, 2, 7, 33, 64, 65, 100, 1000]
+    B, H, D = len(ctx), 2, 64
+    inp = decode_case(B, H, H, D, 16, ctx, seed=1, kv="f32")
+    k0 = np.zeros_like(inp["k"])
+    q, _, v, bt, cd = dev_inputs(inp, dev)
+    k = torch.from_numpy(k0).to(dev)
+    out = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+    for S in (1, 2, 3, 7, 64):
+        ws_bytes = pa.workspace_size(q, k, bt, S)
+        ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        V = pa.view
+        pa.check(pa.lib().pa_v3_partition(C.byref(V(out)), C.byref(V(q)), C.byref(V(k)), C.byref(V(v)),
+                                          C.byref(V(bt)), C.byref(V(cd)), 1.0, S, ws.data_ptr(),
+                                          ws.numel(), torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        if S == 1:
+            continue  # one split is served directly, no workspace
+        rows = B * H * S
+        up = lambda x: (x + 255) // 256 * 256
+        wsh = ws.cpu().numpy()
+        m = wsh[up(rows * D * 4): up(rows * D * 4) + rows * 4].view(np.float32).reshape(B, H, S)
+        l = wsh[up(rows * D * 4) + up(rows * 4): up(rows * D * 4) + up(rows * 4) + rows * 4].view(
+            np.float32).reshape(B, H, S)
+        for b in range(B):
+            for s in range(S):
+                st, en = oracle.partition_bounds(ctx[b], S, s)
+                n = max(0, en - st)
+                assert np.all(l[b, :, s] == n), (S, b, s, l[b, :, s], n)
+                if n == 0:
+                    assert np.all(m[b, :, s] == np.float32(-3.0e38))
+                else:
+                    assert np.all(m[b, :, s] == 0.0)
+
+
+def test_partials_match_oracle_split(pa, dev):
+    """The split pass's partials, in natural-log units, match the reference's
+    split semantics (kernels/paged_attn_v3.cu:33-123) from the oracle."""
+    import ctypes as C
+    ctx = [50, 300, 17]
+    B, H, HKV, D, S = 3, 4, 2, 64, 5
+    inp = decode_case(B, H, HKV, D, 16, ctx, seed=12, kv="f16")
+    q, k, v, bt, cd = dev_inputs(inp, dev)
+    out = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+    ws_bytes = pa.workspace_size(q, k, bt, S)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    V = pa.view
+    pa.check(pa.lib().pa_v3_partition(C.byref(V(out)), C.byref(V(q)), C.byref(V(k)), C.byref(V(v)),
+                                      C.byref(V(bt)), C.byref(V(cd)), 0.125, S, ws.data_ptr(),
+                                      ws.numel(), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    rows = B * H * S
+    up = lambda x: (x + 255) // 256 * 256
+    w = ws.cpu().numpy()
+    acc = w[:rows * D * 4].view(np.float32).reshape(B, H, S, D)
+    m = w[up(rows * D * 4): up(rows * D * 4) + rows * 4].view(np.float32).reshape(B, H, S)
+    l = w[up(rows * D * 4) + up(rows * 4):][:rows * 4].view(np.float32).reshape(B, H, S)
+    pacc, pm, pl = oracle.decode_partials(inp["q_f32"], inp["k"], inp["v"], inp["bt"], inp["ctx"],
+                                          0.125, S, "f16")
+    live = pl > 0
+    assert np.array_equal(live, l > 0)
+    m_nat = m * np.float32(np.log(2.0))
+    close(m_nat[live], pm[live], atol=1e-5, rtol=1e-5)
+    # Kernel partials are relative to its own max: acc_ref = acc_kernel * e^(m_kernel - m_ref).
+    f = np.exp(m_nat - pm)
+    close((l * f)[live], pl[live], atol=1e-4, rtol=1e-4)
+    close((acc * f[..., None])[live], pacc[live], atol=1e-3, rtol=1e-3)

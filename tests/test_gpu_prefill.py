@@ -1,0 +1,125 @@
+"""GPU parity of the prefill entry points against the CPU oracle.
+
+paged_attention_prefill (fp32 arithmetic) and paged_attention_prefill_wmma
+(MFMA, Q and P rounded to the 16-bit KV type) are both checked against the
+oracle's restatement of kernels/paged_attn_prefill.cu:33-118 on the same
+host buffers, for S == ctx (plain causal), S < ctx (chunked prefill: the
+chunk is the trailing S tokens) and S > ctx (padded rows, q_pos < 0 -> 0).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _helpers import ATOL32, RTOL32, close, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def prefill_case(B, S, H, HKV, D, BS, ctx, *, seed, kv="f16", qt="f32"):
+    inp = oracle.paged_inputs(B, 1, HKV, D, BS, ctx, seed=seed, kv_dtype=kv)
+    rng = np.random.default_rng(seed + 1000)
+    q32 = rng.standard_normal((B, S, H, D), dtype=np.float32)
+    q = oracle.quantize(q32, qt)
+    inp.update(q=q, q_f32=oracle.to_float(q, qt), kv=kv, qt=qt)
+    return inp
+
+
+def dev_args(inp, dev):
+    return (to_dev(inp["q"], inp["qt"], dev), to_dev(inp["k"], inp["kv"], dev),
+            to_dev(inp["v"], inp["kv"], dev), torch.from_numpy(inp["bt"]).to(dev),
+            torch.from_numpy(inp["ctx"]).to(dev))
+
+
+def want_of(inp, scale):
+    return oracle.prefill(inp["q_f32"], inp["k"], inp["v"], inp["bt"], inp["ctx"], scale, inp["kv"])
+
+
+SHAPES = [  # (B, S, ctx list)
+    (2, 64, [64, 64]),        # causal, one tile
+    (1, 200, [200]),          # causal, ragged last tile
+    (3, 50, [50, 120, 300]),  # chunked prefill: trailing 50 tokens
+    (2, 40, [25, 0]),         # padded rows (q_pos < 0) and an empty sequence
+]
+
+
+@pytest.mark.parametrize("kv", ["f16", "bf16"])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"B{s[0]}S{s[1]}")
+def test_mfma_prefill(pa, dev, kv, D, shape):
+    B, S, ctx = shape
+    inp = prefill_case(B, S, 4, 2, D, 16, ctx, seed=D + S, kv=kv)
+    scale = 1.0 / np.sqrt(D)
+    got = pa.paged_attention_prefill_wmma(*dev_args(inp, dev), scale)
+    close(to_host(got), want_of(inp, scale))
+
+
+@pytest.mark.parametrize("BS", [8, 16, 32, 7])
+def test_mfma_prefill_block_sizes(pa, dev, BS):
+    inp = prefill_case(2, 100, 6, 3, 64, BS, [100, 180], seed=BS, kv="f16")
+    got = pa.paged_attention_prefill_wmma(*dev_args(inp, dev), 0.125)
+    close(to_host(got), want_of(inp, 0.125))
+
+
+@pytest.mark.parametrize("qt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("ot", [torch.float32, torch.float16, torch.bfloat16])
+def test_mfma_prefill_dtypes(pa, dev, qt, ot):
+    inp = prefill_case(2, 70, 4, 4, 64, 16, [70, 90], seed=7, kv="bf16", qt=qt)
+    got = pa.paged_attention_prefill_wmma(*dev_args(inp, dev), 0.125, out_dtype=ot)
+    assert got.dtype == ot
+    close(to_host(got), want_of(inp, 0.125))
+
+
+def test_mfma_prefill_config4a_shape(pa, dev):
+    """BASELINE config 4a geometry (H=12, D=64, fp16, BS=16, S=ctx=1024), batch 2."""
+    inp = prefill_case(2, 1024, 12, 12, 64, 16, [1024, 1024], seed=44, kv="f16", qt="f16")
+    got = pa.paged_attention_prefill_wmma(*dev_args(inp, dev), 0.125)
+    close(to_host(got), want_of(inp, 0.125))
+
+
+def test_mfma_prefill_vs_torch_sdpa(pa, dev):
+    """ctx == S: plain causal attention, pinned to torch's CPU SDPA (is_causal) on the gathered cache."""
+    B, S, H, D, BS = 2, 96, 4, 64, 16
+    inp = prefill_case(B, S, H, H, D, BS, [S, S], seed=5, kv="f16", qt="f16")
+    got = to_host(pa.paged_attention_prefill_wmma(*dev_args(inp, dev), 0.125))
+    for b in range(B):
+        k = np.stack([oracle.gather(inp["k"], inp["v"], inp["bt"][b], S, h, "f16")[0] for h in range(H)])
+        v = np.stack([oracle.gather(inp["k"], inp["v"], inp["bt"][b], S, h, "f16")[1] for h in range(H)])
+        qb = torch.from_numpy(inp["q_f32"][b].transpose(1, 0, 2).copy()).double()
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            qb, torch.from_numpy(k).double(), torch.from_numpy(v).double(), is_causal=True,
+            scale=0.125)
+        close(got[b], ref.numpy().transpose(1, 0, 2))
+
+
+@pytest.mark.parametrize("kv", ["f32", "f16", "bf16", "f64"])
+def test_fp32_prefill(pa, dev, kv):
+    """paged_attention_prefill keeps fp32 arithmetic: fp32 tolerance on fp32 data."""
+    inp = prefill_case(3, 33, 8, 2, 64, 16, [33, 100, 20], seed=3, kv=kv)
+    got = pa.paged_attention_prefill(*dev_args(inp, dev), 0.2)
+    tol = dict(atol=ATOL32, rtol=RTOL32) if kv in ("f32", "f64") else {}
+    close(to_host(got), want_of(inp, 0.2), **tol)
+
+
+@pytest.mark.parametrize("D", [32, 128, 256])
+def test_fp32_prefill_dims(pa, dev, D):
+    inp = prefill_case(2, 17, 4, 4, D, 8, [17, 40], seed=D, kv="f16")
+    got = pa.paged_attention_prefill(*dev_args(inp, dev), 0.1)
+    close(to_host(got), want_of(inp, 0.1))
+
+
+def test_prefill_bad_block_and_long_context(pa, dev):
+    """A row is NaN iff its sequence's context exceeds the table or a page the
+    row attends has an invalid block id; other rows are unaffected."""
+    inp = prefill_case(3, 40, 4, 4, 64, 16, [40, 40, 40], seed=9, kv="f16")
+    bt = inp["bt"].copy()
+    bt[1, 1] = 10 ** 6          # keys 16..31 of sequence 1: rows 16.. are poisoned
+    ctx = inp["ctx"].copy()
+    ctx[2] = bt.shape[1] * 16 + 1
+    q, k, v, _, _ = dev_args(inp, dev)
+    want = oracle.prefill(inp["q_f32"], inp["k"], inp["v"], bt, ctx, 0.1, "f16")
+    assert np.all(np.isnan(want[1, 16:])) and not np.isnan(want[1, :16]).any()
+    for fn in (pa.paged_attention_prefill, pa.paged_attention_prefill_wmma):
+        got = to_host(fn(q, k, v, torch.from_numpy(bt).to(dev), torch.from_numpy(ctx).to(dev), 0.1))
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        close(got, want)
