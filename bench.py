@@ -1,0 +1,431 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged-attention hot path on one MI355X.
+
+Headline (the JSON line's `value`): BASELINE config 2 -- GPT-2 geometry paged
+decode through paged_attention_v3 (H=12, D=64, BS=16, B=64, ctx=2048, fp16),
+with several disjoint KV pools rotated per step so the working set is well
+above the 256 MB Infinity Cache and every K/V byte comes from HBM.
+
+A step is one paged_attention_v3 call (partition kernel, plus the reduce
+kernel when the plan splits) on one pool, inputs resident in HBM.  `value` is
+algorithmic bytes per step (K and V of every live token once, plus q, out,
+block tables and context lengths) / measured time per step.  The dominant
+kernel's duration is measured with HIP events recorded on the launch stream
+around each partition launch inside the same timed loop.
+
+Also measured (the "also" list): config 3 (GQA bf16 ragged decode), config 5
+(77 GB pool, 64-bit offsets), configs 4a/4b (MFMA causal prefill, TFLOP/s).
+
+cpu_baseline: the reference's own scalar cpu_reference
+(rocm/hip/paged_attn_v1_hip.cpp:104-141, built into oracle/_ref), one thread,
+on a bounded sample of config 2's sequences, timed on this host; the GPU
+result for the sample is checked against it.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload decode_c2]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+import __graft_entry__  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0           # MI355X HBM3E, published
+PEAK_MFMA_TFLOPS = 2500.0       # MI355X dense fp16/bf16 MFMA, published
+METRIC = "decode achieved HBM GB/s (% of 8 TB/s) cold-pool; prefill TFLOP/s (% MFMA peak)"
+PROFILES = ROOT / "profiles"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ decode --
+
+class DecodeWorkload:
+    """Paged decode with `pools` disjoint K/V pools, each holding every page of the batch."""
+
+    def __init__(self, pa, *, B, H, HKV, D, BS, ctx, dtype, pools, seed, name, q_dtype=None,
+                 out_dtype=None, pool_tensor=None):
+        self.pa, self.name = pa, name
+        self.B, self.H, self.HKV, self.D, self.BS = B, H, HKV, D, BS
+        self.dtype = dtype
+        dev = torch.device("cuda:0")
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        self.ctx_host = np.asarray(ctx, np.int32)
+        pages = [-(-int(c) // BS) for c in self.ctx_host]
+        self.MB = max(pages)
+        nb = sum(pages)
+        self.k, self.v, self.bt = [], [], []
+        rng = np.random.default_rng(seed)
+        for p in range(pools):
+            if pool_tensor is not None:
+                k, v = pool_tensor(p)
+            else:
+                k = torch.randn((nb, BS, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+                v = torch.randn((nb, BS, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+            nbp = k.shape[0]
+            perm = rng.permutation(nbp)[:nb].astype(np.int32)
+            bt = np.zeros((B, self.MB), np.int32)
+            pos = 0
+            for b in range(B):
+                bt[b, :pages[b]] = perm[pos:pos + pages[b]]
+                pos += pages[b]
+            self.k.append(k)
+            self.v.append(v)
+            self.bt.append(torch.from_numpy(bt).to(dev))
+            self.bt_host = bt if p == 0 else self.bt_host
+        qd = q_dtype or dtype
+        self.q = torch.randn((B, H, D), generator=g, device=dev, dtype=torch.float32).to(qd)
+        self.out = torch.empty((B, H, D), device=dev, dtype=out_dtype or dtype)
+        self.ctx = torch.from_numpy(self.ctx_host).to(dev)
+        self.scale = 1.0 / float(np.sqrt(D))
+        self.pools = pools
+        self.L = pa.lib()
+        ws = pa.workspace_size(self.q, self.k[0], self.bt[0], 0)
+        self.ws = torch.empty(max(ws, 256), dtype=torch.uint8, device=dev)
+        self.ws_bytes = ws
+        self.split = ws > 0
+        V = pa.view
+        self._keep = []
+        self.args = []
+        for p in range(pools):
+            views = [V(self.out), V(self.q), V(self.k[p]), V(self.v[p]), V(self.bt[p]), V(self.ctx)]
+            self._keep.append(views)
+            self.args.append([C.byref(x) for x in views])
+        self.kv_bytes = 2.0 * float(self.ctx_host.clip(min=0).sum()) * HKV * D * self.k[0].element_size()
+        self.bytes = (self.kv_bytes + self.q.numel() * self.q.element_size()
+                      + self.out.numel() * self.out.element_size() + B * self.MB * 4 + B * 4)
+
+    def footprint_gb(self):
+        return sum(t.numel() * t.element_size() for t in self.k + self.v) / 1e9
+
+    def launch(self, i, stream, ev_mid=None):
+        a = self.args[i % self.pools]
+        ws = self.ws.data_ptr()
+        if not self.split:
+            rc = self.L.paged_attention_v3(*a, self.scale, 0, ws, self.ws_bytes, stream)
+        else:
+            rc = self.L.pa_v3_partition(*a, self.scale, 0, ws, self.ws_bytes, stream)
+            if rc == 0 and ev_mid is not None:
+                ev_mid.record()
+            if rc == 0:
+                rc = self.L.pa_v3_reduce(a[0], a[1], a[2], a[4], a[5], 0, ws, self.ws_bytes, stream)
+        if rc != 0:
+            raise RuntimeError(self.pa.last_error())
+
+
+# ----------------------------------------------------------------- prefill --
+
+class PrefillWorkload:
+    """Causal paged prefill: K/V of S prompt tokens written into a paged pool, then attended."""
+
+    def __init__(self, pa, *, B, S, H, HKV, D, BS, dtype, seed, name):
+        self.pa, self.name = pa, name
+        dev = torch.device("cuda:0")
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        pages = -(-S // BS)
+        nb = B * pages
+        rng = np.random.default_rng(seed)
+        perm = rng.permutation(nb).astype(np.int32).reshape(B, pages)
+        self.q = torch.randn((B, S, H, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+        k_new = torch.randn((B, S, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+        v_new = torch.randn((B, S, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+        # Write the prompt's K/V into the paged pool through the block table (untimed setup).
+        self.k = torch.zeros((nb, BS, HKV, D), device=dev, dtype=dtype)
+        self.v = torch.zeros_like(self.k)
+        tok = torch.arange(S, device=dev)
+        bt = torch.from_numpy(perm).to(dev)
+        for b in range(B):
+            blk = bt[b, tok // BS]
+            self.k[blk, tok % BS] = k_new[b]
+            self.v[blk, tok % BS] = v_new[b]
+        self.bt = bt
+        self.ctx = torch.full((B,), S, dtype=torch.int32, device=dev)
+        self.out = torch.empty((B, S, H, D), device=dev, dtype=dtype)
+        self.scale = 1.0 / float(np.sqrt(D))
+        self.flops = 4.0 * D * H * B * S * (S + 1) / 2.0  # causal pairs, QK^T and PV
+        self.dtype = dtype
+        V = pa.view
+        self._views = [V(self.out), V(self.q), V(self.k), V(self.v), V(self.bt), V(self.ctx)]
+        self.args = [C.byref(x) for x in self._views]
+        self.L = pa.lib()
+
+    def launch(self, i, stream, ev_mid=None):
+        rc = self.L.paged_attention_prefill_wmma(*self.args, self.scale, stream)
+        if rc != 0:
+            raise RuntimeError(self.pa.last_error())
+
+
+# ------------------------------------------------------------------ timing --
+
+def timed(work, steps, warmup):
+    """(ms per step, mean dominant-kernel ms) over `steps` launches after `warmup`."""
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    for i in range(warmup):
+        work.launch(i, sp)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    mids = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    split = getattr(work, "split", False)
+    torch.cuda.synchronize()
+    for i in range(steps):
+        starts[i].record(stream)
+        work.launch(warmup + i, sp, mids[i] if split else None)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    total = starts[0].elapsed_time(ends[-1])
+    kern = [starts[i].elapsed_time(mids[i] if split else ends[i]) for i in range(steps)]
+    return total / steps, float(np.mean(kern))
+
+
+def traffic_from_profiles(kernel_key):
+    """HBM bytes per launch from the committed rocprofv3 counter summary, if present."""
+    f = PROFILES / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        d = json.loads(f.read_text())
+        return d.get(kernel_key, {}).get("bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+# ------------------------------------------------------------- cpu baseline --
+
+def cpu_baseline(work, seconds):
+    """The reference's scalar cpu_reference (oracle/_ref), one thread, on a sample of the
+    workload's sequences (all heads, full context), timed on this host.  Also checks the
+    GPU output of those sequences against it."""
+    import oracle
+    from oracle.pa_oracle import _p
+    R = oracle.ref()
+    kind = "reference" if R is not None else "port"
+    nsamp = 2
+    bt = work.bt_host[:nsamp]
+    used = np.unique(bt[bt >= 0])
+    remap = np.full(work.k[0].shape[0], -1, np.int64)
+    remap[used] = np.arange(used.size)
+    k = work.k[0][torch.from_numpy(used).to(work.k[0].device)].float().cpu().numpy()
+    v = work.v[0][torch.from_numpy(used).to(work.v[0].device)].float().cpu().numpy()
+    bts = np.ascontiguousarray(remap[bt].astype(np.int32))
+    ctx = np.ascontiguousarray(work.ctx_host[:nsamp])
+    q = np.ascontiguousarray(work.q[:nsamp].float().cpu().numpy())
+    B, H, D = q.shape
+    NB, BS, HKV, _ = k.shape
+    out = np.zeros((B, H, D), np.float32)
+    if R is not None:
+        h = R.ref_call_create(_p(k), _p(v), _p(q), _p(bts), _p(ctx), B, H, HKV, D, BS, bts.shape[1],
+                              NB, C.c_float(work.scale))
+        run = lambda: R.ref_call_run(h, _p(out))
+    else:
+        def run():
+            out[...] = oracle.decode(q, k, v, bts, ctx, work.scale, "f32")
+    run()  # warm-up and correctness sample
+    torch.cuda.synchronize()
+    work.launch(0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    gpu = work.out[:nsamp].float().cpu().numpy()
+    err = float(np.abs(gpu - out).max())
+    ok = bool(np.allclose(gpu, out, atol=2e-3, rtol=1e-2))
+    n, t0 = 0, time.perf_counter()
+    while True:
+        run()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 10000:
+            break
+    if R is not None:
+        R.ref_call_free(h)
+    sample_bytes = 2.0 * float(ctx.sum()) * HKV * D * work.k[0].element_size()
+    return {
+        "value": round(sample_bytes * n / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
+        "sample": (f"{nsamp} of {work.B} sequences (all {work.H} heads, ctx {int(ctx[0])}), "
+                   f"{n} calls in {el:.1f} s; KV widened to fp32 for the reference's float API, "
+                   f"bytes counted at the GPU's {work.dtype} size"),
+        "check_vs_gpu": {"max_abs": err, "within_tol": ok},
+    }
+
+
+def torch_sdpa_cpu(work, threads):
+    """PyTorch SDPA on the gathered paged layout, on the host CPU (BASELINE CPU path 3)."""
+    torch.set_num_threads(threads)
+    nsamp = 2
+    idx = torch.from_numpy(work.bt_host[:nsamp].reshape(-1).astype(np.int64)).to(work.k[0].device)
+    k = work.k[0][idx].float().cpu().reshape(nsamp, -1, work.HKV, work.D)[:, :int(work.ctx_host[0])]
+    v = work.v[0][idx].float().cpu().reshape(nsamp, -1, work.HKV, work.D)[:, :int(work.ctx_host[0])]
+    q = work.q[:nsamp].float().cpu()[:, :, None, :]
+    kt = k.permute(0, 2, 1, 3).repeat_interleave(work.H // work.HKV, 1).contiguous()
+    vt = v.permute(0, 2, 1, 3).repeat_interleave(work.H // work.HKV, 1).contiguous()
+    torch.nn.functional.scaled_dot_product_attention(q, kt, vt, scale=work.scale)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 2.0:
+        torch.nn.functional.scaled_dot_product_attention(q, kt, vt, scale=work.scale)
+        n += 1
+    el = time.perf_counter() - t0
+    sample_bytes = 2.0 * nsamp * float(work.ctx_host[0]) * work.HKV * work.D * work.k[0].element_size()
+    return {"value": round(sample_bytes * n / el / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "torch_sdpa_gathered", "sample": f"{nsamp} sequences, {n} calls"}
+
+
+# --------------------------------------------------------------- workloads --
+
+def make_c2(pa, pools):
+    return DecodeWorkload(pa, B=64, H=12, HKV=12, D=64, BS=16, ctx=[2048] * 64, dtype=torch.float16,
+                          pools=pools, seed=2, name="decode_c2")
+
+
+def make_c3(pa, pools):
+    ctx = np.random.default_rng(3).integers(1024, 32769, 32)
+    return DecodeWorkload(pa, B=32, H=32, HKV=8, D=128, BS=16, ctx=ctx, dtype=torch.bfloat16,
+                          pools=pools, seed=3, name="decode_c3")
+
+
+def make_c5(pa):
+    """[12 layers, 2, 131072 blocks, 16, 12, 64] fp16 pool (77.3 GB), decode on layer 11."""
+    dev = torch.device("cuda:0")
+    nb = 131072
+    pool = torch.empty((12, 2, nb, 16, 12, 64), dtype=torch.float16, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    flat = pool.view(-1)
+    step = 1 << 30
+    for off in range(0, flat.numel(), step):
+        n = min(step, flat.numel() - off)
+        flat[off:off + n] = torch.randn(n, generator=g, device=dev, dtype=torch.float16)
+    w = DecodeWorkload(pa, B=256, H=12, HKV=12, D=64, BS=16, ctx=[8192] * 256, dtype=torch.float16,
+                       pools=1, seed=5, name="decode_c5", pool_tensor=lambda p: (pool[11, 0], pool[11, 1]))
+    w.pool = pool
+    w.k_offset_elems = pool[11, 0].storage_offset()
+    return w
+
+
+def decode_record(work, steps, warmup):
+    ms, kms = timed(work, steps, warmup)
+    gbs = work.bytes / (ms * 1e-3) / 1e9
+    return ms, kms, {
+        "workload": work.name, "value": round(gbs, 1), "unit": "GB/s",
+        "frac_of_8TBs": round(gbs / PEAK_HBM_GBS, 4), "ms_per_step": round(ms, 5),
+        "kernel_ms": round(kms, 5), "tokens_per_s": round(work.B / (ms * 1e-3), 1),
+        "bytes_per_step": int(work.bytes), "split": work.split,
+        "pools": work.pools, "footprint_GB": round(work.footprint_gb(), 2),
+    }
+
+
+def prefill_record(work, steps, warmup):
+    ms, kms = timed(work, steps, warmup)
+    tf = work.flops / (kms * 1e-3) / 1e12
+    return {
+        "workload": work.name, "value": round(tf, 1), "unit": "TFLOP/s",
+        "frac_of_mfma_peak": round(tf / PEAK_MFMA_TFLOPS, 4), "ms_per_step": round(ms, 5),
+        "kernel_ms": round(kms, 5), "flops_per_step": work.flops,
+        "prompt_tokens_per_s": round(work.q.shape[0] * work.q.shape[1] / (ms * 1e-3), 1),
+        "dtype": str(work.dtype).replace("torch.", ""),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--pools", type=int, default=6, help="rotated KV pools (config 2)")
+    ap.add_argument("--workload", default="decode_c2",
+                    choices=["decode_c2", "decode_c3", "decode_c5", "prefill_c4a", "prefill_c4b"],
+                    help="with --only: run just this workload's kernel loop (for profiling)")
+    ap.add_argument("--only", action="store_true", help="time only --workload, print its record")
+    ap.add_argument("--no-also", action="store_true", help="skip the secondary configs")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(see DESIGN.md, 'How the path would shard').", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    pa = __graft_entry__.load_package()
+
+    if args.only:
+        w = args.workload
+        if w.startswith("prefill"):
+            work = (PrefillWorkload(pa, B=8, S=1024, H=12, HKV=12, D=64, BS=16, dtype=torch.float16, seed=4,
+                                    name="prefill_c4a") if w == "prefill_c4a" else
+                    PrefillWorkload(pa, B=2, S=4096, H=32, HKV=32, D=128, BS=16, dtype=torch.bfloat16,
+                                    seed=6, name="prefill_c4b"))
+            print(json.dumps(prefill_record(work, args.steps, args.warmup)), flush=True)
+        else:
+            work = {"decode_c2": lambda: make_c2(pa, args.pools), "decode_c3": lambda: make_c3(pa, 2),
+                    "decode_c5": lambda: make_c5(pa)}[w]()
+            print(json.dumps(decode_record(work, args.steps, args.warmup)[2]), flush=True)
+        return
+
+    # ---- headline: config 2 ----
+    log("bench: config 2 (GPT-2 decode, B=64 ctx=2048 fp16, rotated pools)")
+    work = make_c2(pa, args.pools)
+    ms, kms, rec = decode_record(work, args.steps, args.warmup)
+    achieved = work.bytes / (kms * 1e-3) / 1e9
+    log(f"bench: {rec['value']} GB/s per step, kernel {kms * 1e3:.1f} us")
+
+    line = {
+        "metric": METRIC, "value": rec["value"], "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic N(0,1), seeded; random-permutation block tables",
+        "config": {"workload": "decode_c2", "batch": 64, "context_len": 2048, "heads": 12,
+                   "kv_heads": 12, "head_dim": 64, "block_size": 16, "kv_dtype": "f16",
+                   "q_dtype": "f16", "out_dtype": "f16", "entry": "paged_attention_v3(num_splits=0)",
+                   "pools": work.pools, "working_set_GB": rec["footprint_GB"],
+                   "split": work.split},
+        "frac_of_peak": rec["frac_of_8TBs"],
+        "tokens_per_s": rec["tokens_per_s"],
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": traffic_from_profiles("decode_c2"),
+                     "kernel": "pa::decode_kernel<KvF16, 64, 1>",
+                     "kernel_ms": round(kms, 5), "bytes_per_launch": int(work.bytes)},
+    }
+    log("bench: cpu baseline (reference cpu_reference, 1 thread)")
+    line["cpu_baseline"] = cpu_baseline(work, args.cpu_seconds)
+    line["cpu_extra"] = [torch_sdpa_cpu(work, 16)]
+    del work
+    torch.cuda.empty_cache()
+
+    also = []
+    if not args.no_also:
+        for make in (lambda: make_c3(pa, 2), lambda: make_c5(pa)):
+            w = make()
+            log(f"bench: {w.name}")
+            also.append(decode_record(w, max(20, args.steps // 4), 5)[2])
+            if w.name == "decode_c5":
+                also[-1]["k_base_offset_elements"] = int(w.k_offset_elems)
+            del w
+            torch.cuda.empty_cache()
+        for name, kw in (("prefill_c4a", dict(B=8, S=1024, H=12, HKV=12, D=64, dtype=torch.float16, seed=4)),
+                         ("prefill_c4b", dict(B=2, S=4096, H=32, HKV=32, D=128, dtype=torch.bfloat16, seed=6))):
+            log(f"bench: {name}")
+            w = PrefillWorkload(pa, BS=16, name=name, **kw)
+            also.append(prefill_record(w, max(20, args.steps // 4), 5))
+            del w
+            torch.cuda.empty_cache()
+    line["also"] = also
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
