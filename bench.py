@@ -172,25 +172,38 @@ class PrefillWorkload:
 # ------------------------------------------------------------------ timing --
 
 def timed(work, steps, warmup):
-    """(ms per step, mean dominant-kernel ms) over `steps` launches after `warmup`."""
+    """(ms per step, mean dominant-kernel ms).
+
+    ms per step: `steps` back-to-back launches after `warmup`, bracketed by a
+    synchronize and one pair of HIP events on the launch stream.  Dominant
+    kernel: a second pass of `steps` launches with an event pair recorded on
+    the launch stream around each partition launch (events between launches
+    add a small gap, so they are kept out of the first pass)."""
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
     for i in range(warmup):
         work.launch(i, sp)
     torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(steps):
+        work.launch(warmup + i, sp)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    per_step = t0.elapsed_time(t1) / steps
+
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     mids = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     split = getattr(work, "split", False)
-    torch.cuda.synchronize()
     for i in range(steps):
         starts[i].record(stream)
-        work.launch(warmup + i, sp, mids[i] if split else None)
+        work.launch(warmup + steps + i, sp, mids[i] if split else None)
         ends[i].record(stream)
     torch.cuda.synchronize()
-    total = starts[0].elapsed_time(ends[-1])
     kern = [starts[i].elapsed_time(mids[i] if split else ends[i]) for i in range(steps)]
-    return total / steps, float(np.mean(kern))
+    return per_step, float(np.mean(kern))
 
 
 def traffic_from_profiles(kernel_key):
@@ -345,7 +358,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--pools", type=int, default=6, help="rotated KV pools (config 2)")
     ap.add_argument("--workload", default="decode_c2",
-                    choices=["decode_c2", "decode_c3", "decode_c5", "prefill_c4a", "prefill_c4b"],
+                    choices=["decode_c2", "decode_c3", "decode_c5", "prefill_c4a", "prefill_c4b",
+                             "copy_calib"],
                     help="with --only: run just this workload's kernel loop (for profiling)")
     ap.add_argument("--only", action="store_true", help="time only --workload, print its record")
     ap.add_argument("--no-also", action="store_true", help="skip the secondary configs")
@@ -363,6 +377,17 @@ def main():
 
     if args.only:
         w = args.workload
+        if w == "copy_calib":
+            # A plain device copy of known size, to scale the FETCH_SIZE / WRITE_SIZE counters.
+            n = 1 << 30
+            src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda")
+            dst = torch.empty_like(src)
+            for _ in range(args.warmup + args.steps):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            print(json.dumps({"workload": "copy_calib", "bytes_read_per_copy": n,
+                              "bytes_written_per_copy": n, "copies": args.warmup + args.steps}), flush=True)
+            return
         if w.startswith("prefill"):
             work = (PrefillWorkload(pa, B=8, S=1024, H=12, HKV=12, D=64, BS=16, dtype=torch.float16, seed=4,
                                     name="prefill_c4a") if w == "prefill_c4a" else

@@ -197,10 +197,17 @@ int check_args(const pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* 
   if (bt->stride[1] != 1 || (B > 1 && bt->stride[0] < MB))
     return fail(PA_ERR_INVALID_ARGUMENT, "block_tables rows must be contiguous");
   if (ctx->stride[0] != 1 && B > 1) return fail(PA_ERR_INVALID_ARGUMENT, "context_lens must be contiguous");
+  if (NB < 1) return fail(PA_ERR_INVALID_ARGUMENT, "k_cache must hold at least one block");
   const int es = dtype_bytes(k->dtype);
   for (const pa_tensor_t* t : {k, v}) {
     if (t->stride[3] != 1)
       return fail(PA_ERR_INVALID_ARGUMENT, "k_cache/v_cache must have a contiguous last dimension");
+    for (int i = 0; i < 3; ++i)
+      if (t->stride[i] < 0) return fail(PA_ERR_UNSUPPORTED, "k_cache/v_cache strides must be non-negative");
+    // Kernels address a row as block * block_stride (64-bit) + token * token_stride
+    // + lane offset (32-bit): the block stride and one block's extent must fit 32 bits.
+    if (t->stride[0] * es >= (1LL << 32) || (BS * t->stride[1] + D) * es >= (1LL << 32))
+      return fail(PA_ERR_UNSUPPORTED, "k_cache/v_cache block or token stride too large");
     for (int i = 0; i < 3; ++i)
       if (((t->stride[i] * es) & 15) != 0 && t->shape[i] > 1)
         return fail(PA_ERR_UNSUPPORTED, "k_cache/v_cache strides must be multiples of 16 bytes");

@@ -28,6 +28,25 @@
 
 #include "pa_device.hpp"
 
+// Loop-structure knobs (compile-time): K/V loads per lane per tile, whether
+// the next tile's loads are issued before the current tile is consumed, and
+// whether K/V loads carry the non-temporal (streaming) hint.
+#ifndef PA_DECODE_NI
+#define PA_DECODE_NI 4
+#endif
+#ifndef PA_DECODE_PIPE
+#define PA_DECODE_PIPE 1
+#endif
+#ifndef PA_DECODE_NT
+#define PA_DECODE_NT 1
+#endif
+#ifndef PA_DECODE_WAVES
+#define PA_DECODE_WAVES 4
+#endif
+#ifndef PA_DECODE_PRIO
+#define PA_DECODE_PRIO 0
+#endif
+
 namespace pa {
 
 template <typename KV, int D>
@@ -36,12 +55,11 @@ struct DecodeShape {
   static constexpr int LPT = D / VEC;          // lanes per token row
   static_assert(LPT >= 1 && LPT <= 64 && (LPT & (LPT - 1)) == 0, "unsupported D/KV combination");
   static constexpr int TPI = 64 / LPT;         // token rows per load instruction
-  static constexpr int NI_RAW = 32 / TPI;
-  static constexpr int NI = NI_RAW < 1 ? 1 : (NI_RAW > 8 ? 8 : NI_RAW);  // loads per K tile
+  static constexpr int NI = PA_DECODE_NI;      // K (and V) loads per lane per tile
   static constexpr int TT = NI * TPI;          // tokens per wave tile
 };
 
-constexpr int kDecodeWaves = 4;
+constexpr int kDecodeWaves = PA_DECODE_WAVES;
 constexpr int kDecodeThreads = 64 * kDecodeWaves;
 constexpr int kBtChunk = 256;  // block-table entries staged in LDS at a time
 
@@ -57,7 +75,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodePara
   __shared__ float s_l[NW][GC];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int slot = lane / LPT;
   const int sub = lane % LPT;
 
@@ -128,81 +146,186 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodePara
   }
   int bad = 0;
 
-  const int64_t k_lane = ((int64_t)kvh * p.k_sh + sub * VEC) * KV::kBytes;
-  const int64_t v_lane = ((int64_t)kvh * p.v_sh + sub * VEC) * KV::kBytes;
-  const int64_t k_sb = p.k_sb * KV::kBytes, k_st = p.k_st * KV::kBytes;
-  const int64_t v_sb = p.v_sb * KV::kBytes, v_st = p.v_st * KV::kBytes;
+  // Byte strides.  The host guarantees block and token strides (and BS times
+  // the token stride) fit 32 bits, so a row address is one 64-bit
+  // multiply-add on the block id plus a 32-bit in-block offset.
+  const char* kbase = static_cast<const char*>(p.k) + (int64_t)kvh * p.k_sh * KV::kBytes;
+  const char* vbase = static_cast<const char*>(p.v) + (int64_t)kvh * p.v_sh * KV::kBytes;
+  const uint32_t k_sb = (uint32_t)(p.k_sb * KV::kBytes), k_st = (uint32_t)(p.k_st * KV::kBytes);
+  const uint32_t v_sb = (uint32_t)(p.v_sb * KV::kBytes), v_st = (uint32_t)(p.v_st * KV::kBytes);
+  const uint32_t lane_off = (uint32_t)(sub * VEC * KV::kBytes);
   const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
   const uint64_t nb = (uint64_t)p.num_blocks;
 
+  // One wave tile in flight: raw K/V rows of NI tokens per lane and which of
+  // them are live (inside the partition, on a page with a valid block id).
+  struct Tile {
+    u32x4_t k[NI], v[NI];
+    uint32_t live;
+  };
+
+  // Issue the loads of the tile starting at token `tile` (block ids from the
+  // LDS-staged chunk starting at page cp).  Every lane loads: a token past
+  // the partition end, or on a page with an invalid block id, reads row 0 of
+  // block 0 (always in bounds, NB >= 1) and is masked out of the softmax.
+  auto issue = [&](int tile, int cp, int ct1, Tile& T) {
+    int blk[NI], off[NI];
+    bool val[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int t = tile + i * TPI + slot;
+      val[i] = t < ct1;
+      const int tt = val[i] ? t : ct1 - 1;
+      const int pg = (int)fastdiv((uint32_t)tt, p.bs_div);
+      off[i] = tt - pg * p.BS;
+      blk[i] = s_bt[pg - cp];
+    }
+    uint32_t live = 0;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const bool okb = (uint64_t)(int64_t)blk[i] < nb;
+      bad |= (val[i] && !okb) ? 1 : 0;
+      const uint32_t bb = okb ? (uint32_t)blk[i] : 0u;
+      const uint32_t oo = okb ? (uint32_t)off[i] : 0u;
+      T.k[i] = load16<PA_DECODE_NT>(kbase, (uint64_t)bb * k_sb + (oo * k_st + lane_off));
+      T.v[i] = load16<PA_DECODE_NT>(vbase, (uint64_t)bb * v_sb + (oo * v_st + lane_off));
+      live |= (val[i] && okb) ? (1u << i) : 0u;
+    }
+    T.live = live;
+    // Keep the loads here: the scheduler would otherwise sink them next to
+    // their uses (to save registers) and serialise memory behind compute.
+    if constexpr (PA_DECODE_PIPE) __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Fast gather.  When BS is a multiple of TPI and tiles start on multiples
+  // of TPI, the TPI rows of one load instruction lie in one page: the page's
+  // block id and row base are wave-uniform (scalar registers) and a lane's
+  // offset into the rows is loop-invariant, so issuing a load costs no
+  // vector ALU work.  A row outside the partition or on an invalid block
+  // reads row `slot` of block 0 (in bounds) and is masked.
+  const uint32_t lane_row_k = (uint32_t)slot * k_st + lane_off;
+  const uint32_t lane_row_v = (uint32_t)slot * v_st + lane_off;
+  auto issue_fast = [&](int tile, int cp, int ct1, Tile& T) {
+    int off0[NI], braw[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {  // all block-id reads first: one LDS round trip per tile
+      const int ti = tile + i * TPI;  // wave-uniform first token of the instruction
+      const int pg = (int)fastdiv((uint32_t)ti, p.bs_div);
+      off0[i] = ti - pg * p.BS;
+      braw[i] = s_bt[min(pg - cp, kBtChunk - 1)];
+    }
+    uint32_t live = 0;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int ti = tile + i * TPI;
+      const int blk = __builtin_amdgcn_readfirstlane(braw[i]);
+      const bool inrange = ti < ct1;
+      const bool okb = inrange && (uint64_t)(int64_t)blk < nb;
+      bad |= (inrange && !okb) ? 1 : 0;
+      const uint32_t use = okb ? 1u : 0u;
+      const uint64_t rk = (uint64_t)((uint32_t)blk * use) * k_sb + (uint32_t)off0[i] * use * k_st;
+      const uint64_t rv = (uint64_t)((uint32_t)blk * use) * v_sb + (uint32_t)off0[i] * use * v_st;
+      T.k[i] = load16<PA_DECODE_NT>(kbase + rk, lane_row_k);
+      T.v[i] = load16<PA_DECODE_NT>(vbase + rv, lane_row_v);
+      live |= (okb && ti + slot < ct1) ? (1u << i) : 0u;
+    }
+    T.live = live;
+    if constexpr (PA_DECODE_PIPE) __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Online-softmax update of this lane group's streams with one tile.
+  auto consume = [&](const Tile& T) {
+    float s[NI][GC];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      float kf[VEC];
+      KV::widen(T.k[i], kf);
+#pragma unroll
+      for (int g = 0; g < GC; ++g) {
+        float d = 0.0f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) d = fmaf(qr[g][e], kf[e], d);
+        s[i][g] = group_sum<LPT>(d);
+      }
+    }
+    float vf[NI][VEC];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) KV::widen(T.v[i], vf[i]);
+#pragma unroll
+    for (int g = 0; g < GC; ++g) {
+      float mt = kNegBig;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) mt = ((T.live >> i) & 1u) ? fmaxf(mt, s[i][g]) : mt;
+      const float mn = fmaxf(m[g], mt);
+      const float corr = fast_exp2(m[g] - mn);
+      float lg = l[g] * corr;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[g][e] *= corr;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const float pi = ((T.live >> i) & 1u) ? fast_exp2(s[i][g] - mn) : 0.0f;
+        lg += pi;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[g][e] = fmaf(pi, vf[i][e], acc[g][e]);
+      }
+      l[g] = lg;
+      m[g] = mn;
+    }
+  };
+
+  const bool fast = (p.BS % TPI) == 0 && (t0 % TPI) == 0;
   if (t0 < t1) {
     const int pg0 = (int)fastdiv((uint32_t)t0, p.bs_div);
     const int pg1 = (int)fastdiv((uint32_t)(t1 - 1), p.bs_div) + 1;
     for (int cp = pg0; cp < pg1; cp += kBtChunk) {
       const int np = min(kBtChunk, pg1 - cp);
       __syncthreads();
-      if ((int)threadIdx.x < np) s_bt[threadIdx.x] = bt_row[cp + threadIdx.x];
+      for (int i = threadIdx.x; i < np; i += kDecodeThreads) s_bt[i] = bt_row[cp + i];
       __syncthreads();
       const int ct0 = max(t0, cp * p.BS);
       const int ct1 = min(t1, (cp + np) * p.BS);
-      for (int tile = ct0 + wave * TT; tile < ct1; tile += NW * TT) {
-        u32x4_t rk[NI], rv[NI];
-        bool val[NI];
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          const int t = tile + i * TPI + slot;
-          val[i] = t < ct1;
-          rk[i] = u32x4_t{0, 0, 0, 0};
-          rv[i] = u32x4_t{0, 0, 0, 0};
-          if (val[i]) {
-            const int pg = (int)fastdiv((uint32_t)t, p.bs_div);
-            const int off = t - pg * p.BS;
-            const int blk = s_bt[pg - cp];
-            if ((uint64_t)(int64_t)blk >= nb) {
-              bad = 1;
-              val[i] = false;
-            } else {
-              rk[i] = load16(p.k, (int64_t)blk * k_sb + (int64_t)off * k_st + k_lane);
-              rv[i] = load16(p.v, (int64_t)blk * v_sb + (int64_t)off * v_st + v_lane);
-            }
+      // Two tiles per wave in flight: the loads of the next tile are issued
+      // before the current one is consumed.  The next-tile issue is
+      // unconditional (past the end it reads the masked safe row), so every
+      // path reaching a consume has the same loads outstanding and the wait
+      // before it covers only the current tile.
+      auto sweep = [&](auto&& iss) {
+        constexpr int kStep = NW * TT;
+        const int first = ct0 + wave * TT;
+        if constexpr (!PA_DECODE_PIPE) {
+          for (int tile = first; tile < ct1; tile += kStep) {
+            Tile A;
+            iss(tile, cp, ct1, A);
+            consume(A);
           }
-        }
-        float s[NI][GC];
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          float kf[VEC];
-          KV::widen(rk[i], kf);
-#pragma unroll
-          for (int g = 0; g < GC; ++g) {
-            float d = 0.0f;
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) d = fmaf(qr[g][e], kf[e], d);
-            s[i][g] = group_sum<LPT>(d);
+        } else if (first < ct1) {
+          // Counted, branch-free body: tile j+1 is issued before tile j is
+          // consumed.  Every entry of the loop header has exactly one tile
+          // (in A) outstanding, so the waits stay partial.
+          const int ntw = (ct1 - first + kStep - 1) / kStep;  // tiles of this wave
+          Tile A, B;
+          int tile = first;
+          if constexpr (PA_DECODE_PRIO) __builtin_amdgcn_s_setprio(3);
+          iss(tile, cp, ct1, A);
+          if constexpr (PA_DECODE_PRIO) __builtin_amdgcn_s_setprio(0);
+          for (int j = 0; j + 1 < ntw; j += 2) {
+            if constexpr (PA_DECODE_PRIO) __builtin_amdgcn_s_setprio(3);
+            iss(tile + kStep, cp, ct1, B);
+            if constexpr (PA_DECODE_PRIO) __builtin_amdgcn_s_setprio(0);
+            consume(A);
+            if constexpr (PA_DECODE_PRIO) __builtin_amdgcn_s_setprio(3);
+            iss(tile + 2 * kStep, cp, ct1, A);
+            if constexpr (PA_DECODE_PRIO) __builtin_amdgcn_s_setprio(0);
+            consume(B);
+            tile += 2 * kStep;
           }
+          if (ntw & 1) consume(A);
         }
-        float vf[NI][VEC];
-#pragma unroll
-        for (int i = 0; i < NI; ++i) KV::widen(rv[i], vf[i]);
-#pragma unroll
-        for (int g = 0; g < GC; ++g) {
-          float mt = kNegBig;
-#pragma unroll
-          for (int i = 0; i < NI; ++i) mt = val[i] ? fmaxf(mt, s[i][g]) : mt;
-          const float mn = fmaxf(m[g], mt);
-          const float corr = fast_exp2(m[g] - mn);
-          float lg = l[g] * corr;
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) acc[g][e] *= corr;
-#pragma unroll
-          for (int i = 0; i < NI; ++i) {
-            const float pi = val[i] ? fast_exp2(s[i][g] - mn) : 0.0f;
-            lg += pi;
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) acc[g][e] = fmaf(pi, vf[i][e], acc[g][e]);
-          }
-          l[g] = lg;
-          m[g] = mn;
-        }
+      };
+      if (fast) {
+        sweep(issue_fast);
+      } else {
+        sweep(issue);
       }
     }
   }

@@ -63,8 +63,11 @@ struct KvF64 {
   }
 };
 
+template <int NT = 0>
 __device__ inline u32x4_t load16(const void* base, int64_t byte_off) {
-  return *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(base) + byte_off);
+  const u32x4_t* ptr = reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(base) + byte_off);
+  if constexpr (NT) return __builtin_nontemporal_load(ptr);
+  return *ptr;
 }
 
 // ------------------------------------------------------- scalar element I/O --
