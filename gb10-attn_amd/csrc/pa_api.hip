@@ -468,6 +468,8 @@ int paged_attention_prefill_wmma(pa_tensor_t* out, const pa_tensor_t* q,
     return fail(PA_ERR_INVALID_ARGUMENT, "the MFMA path needs an fp16 or bf16 KV cache");
   if (a.p.D > 256) return fail(PA_ERR_UNSUPPORTED, "unsupported head_dim for the MFMA path: %d", a.p.D);
   if ((int64_t)a.p.B * a.p.Sq * a.p.H == 0) return PA_OK;
+  if ((reinterpret_cast<uintptr_t>(q->data) & 15) != 0)
+    return fail(PA_ERR_UNSUPPORTED, "the MFMA path needs a 16-byte aligned q");
   PrefillParams pp;
   memset(&pp, 0, sizeof(pp));
   const DecodeParams& p = a.p;

@@ -42,10 +42,6 @@ namespace pa {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kPfQB = 64;  // query rows per work-group
-constexpr int kPfKB = 64;  // keys per tile
-constexpr int kPfThreads = 256;
-
 template <typename KV>
 __device__ inline float4_t mfma16x16x32(const u32x4_t& a, const u32x4_t& b, const float4_t& c) {
   if constexpr (KV::kCode == kF16) {
@@ -67,6 +63,26 @@ __device__ inline uint32_t to_bits16(float x) {
   }
 }
 
+// Eight consecutive q elements (16-byte aligned) as fp32.
+__device__ inline void load8f(const void* q, int dtype, int64_t idx, float (&x)[8]) {
+  if (dtype == kF32) {
+    const float4_t a = *reinterpret_cast<const float4_t*>(static_cast<const float*>(q) + idx);
+    const float4_t b = *reinterpret_cast<const float4_t*>(static_cast<const float*>(q) + idx + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = a[e];
+      x[4 + e] = b[e];
+    }
+  } else {
+    const u32x4_t r = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(q) + idx);
+    if (dtype == kF16) {
+      KvF16::widen(r, x);
+    } else {
+      KvBF16::widen(r, x);
+    }
+  }
+}
+
 template <typename KV>
 __device__ inline float from_bits16(uint32_t h) {
   if constexpr (KV::kCode == kF16) {
@@ -76,25 +92,58 @@ __device__ inline float from_bits16(uint32_t h) {
   }
 }
 
-template <typename KV, int D>
-__global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillParams p) {
-  constexpr int NSLAB = D / 32;         // 32-wide k-slabs of the QK^T product
-  constexpr int NDT = D / 16;           // 16-row tiles of O^T
-  constexpr int KROW = D + 8;           // sK row pitch (elements): 16-byte pad
-  constexpr int VROW = kPfKB + 8;       // sV row pitch (keys)
-  constexpr int CHUNKS = kPfKB * D / 8; // 16-byte pieces per K (or V) tile
-  constexpr int CPT = (CHUNKS + kPfThreads - 1) / kPfThreads;
-  static_assert(D % 32 == 0, "D must be a multiple of 32");
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
-  __shared__ __attribute__((aligned(16))) uint16_t sK[kPfKB * KROW];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[D * VROW];
+constexpr int kPfThreads = 256;  // 4 waves
+constexpr int kPfBtStage = 1024;  // block-table entries staged in LDS
+
+// Query rows per wave for head dims up to 128 (compile-time knob): 32 gives
+// each LDS K/V fragment two uses, 16 halves the registers.
+#ifndef PA_PF_QW
+#define PA_PF_QW 32
+#endif
+
+template <int D>
+struct PfShape {
+  static constexpr int QW = D <= 128 ? PA_PF_QW : 16;  // query rows per wave
+  static constexpr int NT = QW / 16;             // 16-column n-tiles per wave
+  static constexpr int QB = 4 * QW;              // query rows per work-group
+  static constexpr int KB = D <= 128 ? 64 : 32;  // keys per tile
+  static constexpr int MT = KB / 16;             // 16-key m-tiles per tile
+  static constexpr int NSLAB = D / 32;           // 32-wide k-slabs of Q.K^T
+  static constexpr int NDT = D / 16;             // 16-row tiles of O^T
+  static constexpr int NCH = D / 8;              // 16-byte chunks per row
+  static constexpr int SWZ = NCH >= 8 ? 7 : NCH - 1;  // chunk swizzle mask
+  static constexpr int CPT = KB * NCH / kPfThreads;    // chunks per thread per tile
+  static_assert(KB * NCH % kPfThreads == 0, "tile chunks must divide the work-group");
+};
+
+// LDS element offset of (row, chunk cc) in a swizzled [KB][D] tile: chunk cc of
+// row r lives at chunk position cc ^ (r & SWZ), which spreads the 16-byte
+// reads of 16 consecutive rows (same cc) over distinct banks.
+template <int D>
+__device__ inline int swz(int row, int cc) {
+  return row * D + ((cc ^ (row & PfShape<D>::SWZ)) << 3);
+}
+
+template <typename KV, int D, bool kSplitQ>
+__global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillParams p) {
+  using Sh = PfShape<D>;
+  constexpr int QW = Sh::QW, NT = Sh::NT, QB = Sh::QB, KB = Sh::KB, MT = Sh::MT;
+  constexpr int NSLAB = Sh::NSLAB, NDT = Sh::NDT, NCH = Sh::NCH, CPT = Sh::CPT;
+
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][KB * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][KB * D];
+  __shared__ int s_badkey;  // first key whose page has an invalid block id
+  __shared__ int32_t s_bt[kPfBtStage];  // the work-group's block ids, when they fit
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15;  // query column (S^T / O^T) or key row (K operand)
   const int kg = lane >> 4;   // lane group: k-index block of the operands
 
-  // Work-group -> (b, h, query tile): XCD-contiguous, longest tile first.
+  // Work-group -> (b, h, query block): XCD-contiguous, longest block first.
   const int nq = p.q_tiles;
   const int64_t total = (int64_t)p.B * p.H * nq;
   int64_t x = blockIdx.x;
@@ -107,216 +156,308 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
 
   const int ctx = p.context_lens[b];
   const int maxctx = p.MB * p.BS;
-  const int qs0 = qt * kPfQB;
-  const int qrow = qs0 + wave * 16 + col;           // this lane's query row
-  const bool row_live = qrow < p.S;
-  const int qpos = ctx - p.S + qrow;                // absolute position
-  const int64_t out_row = (((int64_t)b * p.S + qrow) * p.H + h) * D;
+  const int qs0 = qt * QB;
+  const int qw0 = qs0 + wave * QW;  // this wave's first query row
 
-  if (ctx > maxctx) {  // context longer than the block table: poison the rows that attend keys
-    if (row_live && kg == 0) {
-      const float fillv = qpos < 0 ? 0.0f : __builtin_nanf("");
-      for (int d = 0; d < D; ++d) store_elem(p.out, p.out_dtype, out_row + d, fillv);
+  if (ctx > maxctx) {  // context longer than the block table: poison rows that attend keys
+    for (int nt = 0; nt < NT; ++nt) {
+      const int qrow = qw0 + nt * 16 + col;
+      if (qrow < p.S && kg == 0) {
+        const float fillv = ctx - p.S + qrow < 0 ? 0.0f : __builtin_nanf("");
+        const int64_t orow = (((int64_t)b * p.S + qrow) * p.H + h) * D;
+        for (int d = 0; d < D; ++d) store_elem(p.out, p.out_dtype, orow + d, fillv);
+      }
     }
     return;
   }
-  __shared__ int s_badkey;  // first key whose page has an invalid block id
   if (threadIdx.x == 0) s_badkey = 0x7fffffff;
-  __syncthreads();
-  // Keys the whole work-group can see: [0, kend).
-  const int kend = min(ctx, ctx - p.S + min(qs0 + kPfQB, p.S));
-  const int ntiles = kend > 0 ? (kend + kPfKB - 1) / kPfKB : 0;
-  // Keys this wave's rows can see.
-  const int wave_last = min(qs0 + wave * 16 + 15, p.S - 1);
-  const int wave_kend = min(ctx, ctx - p.S + wave_last + 1);
-  const int wave_kfull = ctx - p.S + qs0 + wave * 16 + 1;  // keys < this are visible to all rows
 
-  // Q^T operand: row qrow, dims c*32 + kg*8 .. +8, rounded to the KV type
-  // (qf) with the rounding residual in qf_lo.
-  u32x4_t qf[NSLAB], qf_lo[NSLAB];
+  // Keys the work-group's rows can see: [0, kend); this wave's rows: [0, wave_kend).
+  const int kend = min(ctx, ctx - p.S + min(qs0 + QB, p.S));
+  const int ntiles = kend > 0 ? (kend + KB - 1) / KB : 0;
+  const int wave_last = min(qw0 + QW - 1, p.S - 1);
+  const int wave_kend = min(ctx, ctx - p.S + wave_last + 1);
+  const int wave_kfull = ctx - p.S + qw0 + 1;  // keys below this are visible to every row
+  const bool wave_padded = qw0 + QW > p.S;
+
+  // Q^T operands (rows qw0 + nt*16 + col, dims c*32 + kg*8 .. +8), rounded to
+  // the KV type, with the rounding residual for the low-part product.
+  u32x4_t qf[NT][NSLAB], qf_lo[kSplitQ ? NT : 1][NSLAB];
+  int qpos[NT];
+  bool live[NT];
 #pragma unroll
-  for (int c = 0; c < NSLAB; ++c) {
-    uint32_t w[4], wl[4];
+  for (int nt = 0; nt < NT; ++nt) {
+    const int qrow = qw0 + nt * 16 + col;
+    live[nt] = qrow < p.S;
+    qpos[nt] = ctx - p.S + qrow;
+    const int64_t qrow_off = (((int64_t)b * p.S + qrow) * p.H + h) * D;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float x0 = 0.0f, x1 = 0.0f;
-      if (row_live) {
-        const int64_t qi = out_row + c * 32 + kg * 8 + 2 * j;
-        x0 = load_elem(p.q, p.q_dtype, qi);
-        x1 = load_elem(p.q, p.q_dtype, qi + 1);
+    for (int c = 0; c < NSLAB; ++c) {
+      uint32_t w[4], wl[4];
+      float xv[8];
+      if (live[nt]) {
+        load8f(p.q, p.q_dtype, qrow_off + c * 32 + kg * 8, xv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[e] = 0.0f;
       }
-      const uint32_t h0 = to_bits16<KV>(x0), h1 = to_bits16<KV>(x1);
-      w[j] = h0 | (h1 << 16);
-      wl[j] = to_bits16<KV>(x0 - from_bits16<KV>(h0)) | (to_bits16<KV>(x1 - from_bits16<KV>(h1)) << 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float x0 = xv[2 * j], x1 = xv[2 * j + 1];
+        const uint32_t h0 = to_bits16<KV>(x0), h1 = to_bits16<KV>(x1);
+        w[j] = h0 | (h1 << 16);
+        wl[j] = to_bits16<KV>(x0 - from_bits16<KV>(h0)) | (to_bits16<KV>(x1 - from_bits16<KV>(h1)) << 16);
+      }
+      qf[nt][c] = u32x4_t{w[0], w[1], w[2], w[3]};
+      if constexpr (kSplitQ) qf_lo[nt][c] = u32x4_t{wl[0], wl[1], wl[2], wl[3]};
     }
-    qf[c] = u32x4_t{w[0], w[1], w[2], w[3]};
-    qf_lo[c] = u32x4_t{wl[0], wl[1], wl[2], wl[3]};
   }
-  const bool q_split = p.q_split != 0;
   constexpr bool kSplitP = KV::kCode == kBF16;
 
-  float4_t o[NDT];
+  float4_t o[NDT][NT];
 #pragma unroll
-  for (int t = 0; t < NDT; ++t) o[t] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m = kNegBig;
-  float l = 0.0f;  // this lane group's share of the row sum
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) o[dt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float m[NT], l[NT];  // l: this lane group's share of the row sum
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    m[nt] = kNegBig;
+    l[nt] = 0.0f;
+  }
 
   const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
+  // Block ids of the pages this work-group reads live in an LDS window of
+  // kPfBtStage pages starting at page win0, so a tile's K/V loads never wait
+  // behind a dependent block-table load.  The window moves (at a tile
+  // boundary, behind a barrier) when the next tile to load leaves it.
+  const int npages = kend > 0 ? (int)fastdiv((uint32_t)(kend - 1), p.bs_div) + 1 : 0;
+  int win0 = 0;
+  auto stage = [&](int first) {
+    win0 = first;
+    const int n = min(kPfBtStage, npages - first);
+    for (int i = threadIdx.x; i < n; i += kPfThreads) s_bt[i] = bt_row[first + i];
+  };
+  auto ensure_window = [&](int t) {  // uniform; call with every thread, then barrier
+    const int last = min(t * KB + KB, kend) - 1;
+    const int plast = (int)fastdiv((uint32_t)last, p.bs_div);
+    if (plast >= win0 + kPfBtStage) {
+      __syncthreads();  // every gload of the old window is done
+      stage((int)fastdiv((uint32_t)(t * KB), p.bs_div));
+      __syncthreads();
+    }
+  };
+  stage(0);
+  __syncthreads();
   const int64_t k_sb = p.k_sb * 2, k_st = p.k_st * 2, k_sh = (int64_t)kvh * p.k_sh * 2;
   const int64_t v_sb = p.v_sb * 2, v_st = p.v_st * 2, v_sh = (int64_t)kvh * p.v_sh * 2;
   const uint64_t nb = (uint64_t)p.num_blocks;
+  int badkey = 0x7fffffff;
 
+  // Global -> registers for tile t (16-byte chunks), registers -> LDS (swizzled).
+  // Global -> registers for tile t.  Branch-free: a row past kend, or on a
+  // page with an invalid block id, loads row 0 of block 0 (in bounds, NB >= 1)
+  // and is zeroed when stored to LDS.
   u32x4_t rk[CPT], rv[CPT];
-  auto gload = [&](int tile) {
+  uint32_t rmask = 0;
+  const char* kbase = static_cast<const char*>(p.k) + k_sh;
+  const char* vbase = static_cast<const char*>(p.v) + v_sh;
+  auto gload = [&](int t) {
+    int blk[CPT], off[CPT];
+    bool val[CPT];
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
       const int idx = (int)threadIdx.x + c * kPfThreads;
-      rk[c] = u32x4_t{0, 0, 0, 0};
-      rv[c] = u32x4_t{0, 0, 0, 0};
-      if (idx < CHUNKS) {
-        const int key = idx / (D / 8);
-        const int dg = idx - key * (D / 8);
-        const int kabs = tile * kPfKB + key;
-        if (kabs < kend) {
-          const int pg = (int)fastdiv((uint32_t)kabs, p.bs_div);
-          const int off = kabs - pg * p.BS;
-          const int blk = bt_row[pg];
-          if ((uint64_t)(int64_t)blk >= nb) {
-            atomicMin(&s_badkey, kabs);
-          } else {
-            rk[c] = load16(p.k, (int64_t)blk * k_sb + (int64_t)off * k_st + k_sh + dg * 16);
-            rv[c] = load16(p.v, (int64_t)blk * v_sb + (int64_t)off * v_st + v_sh + dg * 16);
-          }
-        }
-      }
+      const int row = idx / NCH;
+      const int kabs = t * KB + row;
+      val[c] = kabs < kend;
+      const int pg = (int)fastdiv((uint32_t)(val[c] ? kabs : 0), p.bs_div);
+      off[c] = (val[c] ? kabs : 0) - pg * p.BS;
+      blk[c] = s_bt[val[c] ? pg - win0 : 0];
+    }
+    uint32_t mask = 0;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int idx = (int)threadIdx.x + c * kPfThreads;
+      const int cc = idx - (idx / NCH) * NCH;
+      const bool okb = (uint64_t)(int64_t)blk[c] < nb;
+      if (val[c] && !okb) badkey = min(badkey, t * KB + idx / NCH);
+      const bool use = val[c] && okb;
+      const int64_t bb = use ? blk[c] : 0;
+      const int64_t oo = use ? off[c] : 0;
+      rk[c] = load16(kbase, bb * k_sb + oo * k_st + cc * 16);
+      rv[c] = load16(vbase, bb * v_sb + oo * v_st + cc * 16);
+      mask |= use ? (1u << c) : 0u;
+    }
+    rmask = mask;
+  };
+  auto sstore = [&](int buf) {
+    const u32x4_t zero = u32x4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int idx = (int)threadIdx.x + c * kPfThreads;
+      const int row = idx / NCH, cc = idx - (idx / NCH) * NCH;
+      const bool use = (rmask >> c) & 1u;
+      *reinterpret_cast<u32x4_t*>(&sK[buf][swz<D>(row, cc)]) = use ? rk[c] : zero;
+      *reinterpret_cast<u32x4_t*>(&sV[buf][swz<D>(row, cc)]) = use ? rv[c] : zero;
     }
   };
 
-  if (ntiles > 0) gload(0);
-  for (int t = 0; t < ntiles; ++t) {
-    // Stage the tile: K as [key][D], V transposed as [D][key].
+  auto compute = [&](int t, int buf) {
+    const int tk0 = t * KB;
+    // S^T = K . Q^T: MT x NT tiles of 16 keys x 16 queries.
+    float4_t st[MT][NT];
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int idx = (int)threadIdx.x + c * kPfThreads;
-      if (idx < CHUNKS) {
-        const int key = idx / (D / 8);
-        const int dg = idx - key * (D / 8);
-        *reinterpret_cast<u32x4_t*>(&sK[key * KROW + dg * 8]) = rk[c];
+    for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          sV[(dg * 8 + 2 * j) * VROW + key] = (uint16_t)(rv[c][j] & 0xffffu);
-          sV[(dg * 8 + 2 * j + 1) * VROW + key] = (uint16_t)(rv[c][j] >> 16);
+      for (int nt = 0; nt < NT; ++nt) st[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NSLAB; ++c) {
+        const int row = mt * 16 + col;
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&sK[buf][swz<D>(row, c * 4 + kg)]);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          st[mt][nt] = mfma16x16x32<KV>(a, qf[nt][c], st[mt][nt]);
+          if constexpr (kSplitQ) st[mt][nt] = mfma16x16x32<KV>(a, qf_lo[nt][c], st[mt][nt]);
         }
       }
     }
-    __syncthreads();
-    if (t + 1 < ntiles) gload(t + 1);
-
-    const int tk0 = t * kPfKB;
-    if (tk0 < wave_kend) {
-      // S^T tile: 4 blocks of 16 keys x 16 query columns.
-      float4_t st[4];
+    // Online softmax per query column; keys of this lane: tk0 + mt*16 + kg*4 + i.
+    const bool need_mask = tk0 + KB > wave_kfull || wave_padded;
+    u32x4_t pb[KB / 32][NT], pb_lo[KB / 32][NT];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < NSLAB; ++c) {
-          const u32x4_t a =
-              *reinterpret_cast<const u32x4_t*>(&sK[(mt * 16 + col) * KROW + c * 32 + kg * 8]);
-          acc = mfma16x16x32<KV>(a, qf[c], acc);
-          if (q_split) acc = mfma16x16x32<KV>(a, qf_lo[c], acc);
-        }
-        st[mt] = acc;
-      }
-      const bool need_mask = tk0 + kPfKB > wave_kfull || !row_live;
+    for (int nt = 0; nt < NT; ++nt) {
       float mx = kNegBig;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float s = st[mt][i] * p.qscale;
+          float sv = st[mt][nt][i] * p.qscale;
           if (need_mask) {
             const int key = tk0 + mt * 16 + kg * 4 + i;
-            if (!(row_live && key <= qpos)) s = kNegBig;
+            if (!(live[nt] && key <= qpos[nt])) sv = kNegBig;
           }
-          st[mt][i] = s;
-          mx = fmaxf(mx, s);
+          st[mt][nt][i] = sv;
+          mx = fmaxf(mx, sv);
         }
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mn = fmaxf(m, mx);
-      const float corr = fast_exp2(m - mn);
-      l *= corr;
+      const float mn = fmaxf(m[nt], mx);
+      const float corr = fast_exp2(m[nt] - mn);
+      m[nt] = mn;
+      float ls = l[nt] * corr;
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
-      // P^T operand, one per 32-key chunk: keys c2*32 + kg*4 + {0..3} and
-      // c2*32 + 16 + kg*4 + {0..3}, matching the V^T reads below.
-      u32x4_t pb[2], pb_lo[2];
+      for (int dt = 0; dt < NDT; ++dt) o[dt][nt] *= corr;
+      // P^T operand per 32-key chunk c2: keys c2*32 + kg*4 + {0..3} (m-tile 2*c2)
+      // then c2*32 + 16 + kg*4 + {0..3} (m-tile 2*c2+1), matching the V^T reads.
 #pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) {
+      for (int c2 = 0; c2 < KB / 32; ++c2) {
         uint32_t w[4], wl[4];
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            const float s0 = st[2 * c2 + half][2 * j];
-            const float s1 = st[2 * c2 + half][2 * j + 1];
+            const float s0 = st[2 * c2 + half][nt][2 * j];
+            const float s1 = st[2 * c2 + half][nt][2 * j + 1];
             const float p0 = s0 > kNegBig ? fast_exp2(s0 - mn) : 0.0f;
             const float p1 = s1 > kNegBig ? fast_exp2(s1 - mn) : 0.0f;
             const uint32_t h0 = to_bits16<KV>(p0), h1 = to_bits16<KV>(p1);
             w[half * 2 + j] = h0 | (h1 << 16);
             if constexpr (kSplitP) {
-              l += p0 + p1;
+              ls += p0 + p1;
               wl[half * 2 + j] = to_bits16<KV>(p0 - from_bits16<KV>(h0)) |
                                  (to_bits16<KV>(p1 - from_bits16<KV>(h1)) << 16);
             } else {
-              l += from_bits16<KV>(h0) + from_bits16<KV>(h1);
+              ls += from_bits16<KV>(h0) + from_bits16<KV>(h1);
             }
           }
         }
-        pb[c2] = u32x4_t{w[0], w[1], w[2], w[3]};
-        if constexpr (kSplitP) pb_lo[c2] = u32x4_t{wl[0], wl[1], wl[2], wl[3]};
+        pb[c2][nt] = u32x4_t{w[0], w[1], w[2], w[3]};
+        if constexpr (kSplitP) pb_lo[c2][nt] = u32x4_t{wl[0], wl[1], wl[2], wl[3]};
       }
-      m = mn;
+      l[nt] = ls;
+    }
+    // O^T += V^T . P^T.  V^T operand for (c2, dt): two transposing 8-byte LDS
+    // reads; lane j of each 16-lane group supplies row key_base + j/4, dims
+    // dt*16 + (j%4)*4 .. +4, and receives dim dt*16 + j for the 4 rows.
+    const int trow = col >> 2, tcol = (col & 3) * 4;
 #pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) {
+    for (int c2 = 0; c2 < KB / 32; ++c2) {
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          const uint16_t* vr = &sV[(dt * 16 + col) * VROW + c2 * 32 + kg * 4];
-          const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr);
-          const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 16);
-          const u32x4_t a = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
-          o[dt] = mfma16x16x32<KV>(a, pb[c2], o[dt]);
-          if constexpr (kSplitP) o[dt] = mfma16x16x32<KV>(a, pb_lo[c2], o[dt]);
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int r0 = c2 * 32 + kg * 4 + trow;
+        const int r1 = r0 + 16;
+        const int dcol = dt * 16 + tcol;
+        const int e0 = swz<D>(r0, dcol >> 3) + (dcol & 7);
+        const int e1 = swz<D>(r1, dcol >> 3) + (dcol & 7);
+        const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(&sV[buf][e0]));
+        const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(&sV[buf][e1]));
+        const uint64_t lo64 = __builtin_bit_cast(uint64_t, lo), hi64 = __builtin_bit_cast(uint64_t, hi);
+        const u32x4_t a = u32x4_t{(uint32_t)lo64, (uint32_t)(lo64 >> 32), (uint32_t)hi64,
+                                  (uint32_t)(hi64 >> 32)};
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          o[dt][nt] = mfma16x16x32<KV>(a, pb[c2][nt], o[dt][nt]);
+          if constexpr (kSplitP) o[dt][nt] = mfma16x16x32<KV>(a, pb_lo[c2][nt], o[dt][nt]);
         }
       }
     }
-    __syncthreads();
+  };
+
+  // Double-buffered tiles: the next tile's global loads are in flight while
+  // the current tile is computed; one barrier per tile.
+  if (ntiles > 0) {
+    gload(0);
+    sstore(0);
   }
   __syncthreads();
-  const bool bad = s_badkey <= qpos;  // this row read a page with an invalid block id
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) {
+      ensure_window(t + 1);
+      gload(t + 1);
+    }
+    if (t * KB < wave_kend) compute(t, buf);
+    if (t + 1 < ntiles) sstore(buf ^ 1);
+    __syncthreads();
+  }
+  if (badkey != 0x7fffffff) atomicMin(&s_badkey, badkey);
+  __syncthreads();
+  const int bad_from = s_badkey;
 
-  // Row sum over the 4 lane groups, normalise, write 4 dims per lane per O^T tile.
-  float lt = l + __shfl_xor(l, 16, 64);
-  lt += __shfl_xor(lt, 32, 64);
-  if (!row_live) return;
-  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  // Row sums over the 4 lane groups, normalise, write 4 dims per lane per O^T tile.
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) {
+  for (int nt = 0; nt < NT; ++nt) {
+    float lt = l[nt] + __shfl_xor(l[nt], 16, 64);
+    lt += __shfl_xor(lt, 32, 64);
+    if (!live[nt]) continue;
+    const bool bad = bad_from <= qpos[nt];
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    const int qrow = qw0 + nt * 16 + col;
+    const int64_t orow = (((int64_t)b * p.S + qrow) * p.H + h) * D;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = dt * 16 + kg * 4 + i;
-      store_elem(p.out, p.out_dtype, out_row + d, bad ? __builtin_nanf("") : o[dt][i] * inv);
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = dt * 16 + kg * 4 + i;
+        store_elem(p.out, p.out_dtype, orow + d, bad ? __builtin_nanf("") : o[dt][nt][i] * inv);
+      }
     }
   }
 }
 
 template <typename KV, int D>
 static hipError_t launch_pf(const PrefillParams& p, hipStream_t stream) {
-  const int64_t blocks = (int64_t)p.B * p.H * p.q_tiles;
-  hipLaunchKernelGGL((prefill_mfma_kernel<KV, D>), dim3((unsigned)blocks), dim3(kPfThreads), 0,
-                     stream, p);
+  PrefillParams q = p;
+  q.q_tiles = (p.S + PfShape<D>::QB - 1) / PfShape<D>::QB;
+  const int64_t blocks = (int64_t)q.B * q.H * q.q_tiles;
+  if (p.q_split)
+    hipLaunchKernelGGL((prefill_mfma_kernel<KV, D, true>), dim3((unsigned)blocks), dim3(kPfThreads),
+                       0, stream, q);
+  else
+    hipLaunchKernelGGL((prefill_mfma_kernel<KV, D, false>), dim3((unsigned)blocks), dim3(kPfThreads),
+                       0, stream, q);
   return hipGetLastError();
 }
 
