@@ -480,10 +480,24 @@ int paged_attention_prefill_wmma(pa_tensor_t* out, const pa_tensor_t* q,
   pp.bt_stride = p.bt_stride; pp.num_blocks = p.num_blocks;
   pp.B = p.B; pp.S = p.Sq; pp.H = p.H; pp.HKV = p.HKV; pp.G = p.G; pp.D = p.D; pp.BS = p.BS; pp.MB = p.MB;
   pp.q_dtype = p.q_dtype; pp.out_dtype = p.out_dtype;
-  pp.q_tiles = (p.Sq + 63) / 64;
   pp.q_split = p.q_dtype != a.kv_dtype;
   pp.bs_div = p.bs_div;
-  pp.qscale = p.qscale;
+  // The kernel applies the sign of the scale to q (exactly) and keeps the
+  // softmax scale positive, so the running max of raw scores orders as the scaled ones.
+  const double log2e = 1.4426950408889634;
+  pp.q_and = 0xffffffffu;
+  pp.q_xor = 0u;
+  pp.q_sign = 1.0f;
+  pp.qscale = (float)(scale * log2e);
+  if (scale < 0) {
+    pp.q_xor = 0x80008000u;
+    pp.q_sign = -1.0f;
+    pp.qscale = (float)(-scale * log2e);
+  } else if (scale == 0) {
+    pp.q_and = 0u;
+    pp.q_sign = 0.0f;
+    pp.qscale = 1.0f;
+  }
   return hip_status(launch_prefill_mfma(pp, a.kv_dtype, static_cast<hipStream_t>(stream)),
                     "prefill kernel launch");
 }

@@ -91,7 +91,10 @@ struct PrefillParams {
   int32_t q_tiles;   // ceil(S / QBLOCK)
   int32_t q_split;   // q is not exactly the KV type: add a low-part product
   FastDiv bs_div;
-  float qscale;      // scale * log2(e)
+  float qscale;      // |scale| * log2(e), or 1 when scale == 0 (always positive)
+  float q_sign;      // sign of scale applied to q (+1, -1, or 0 when scale == 0)
+  uint32_t q_and;    // the same on packed 16-bit q: bits & q_and ^ q_xor
+  uint32_t q_xor;
 };
 
 // Host launchers (defined in the kernel translation units).

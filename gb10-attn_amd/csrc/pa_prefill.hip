@@ -1,27 +1,31 @@
 // pa_prefill.hip -- causal paged prefill on CDNA4 matrix cores (gfx950).
 //
 // Replaces the reference's WMMA tile kernel (kernels/paged_attn_wmma.cu:36-210)
-// with a design built around v_mfma_f32_16x16x32_{f16,bf16}:
+// with a design built around v_mfma_f32_32x32x16_{f16,bf16}:
 //
-//  * A work-group (4 waves) owns one (sequence b, query head h, block of 64
-//    query rows); wave w owns 16 of those rows.  Key tiles of 64 keys are
-//    gathered from the paged pool (block table -> page -> row, 64-bit offsets)
-//    into LDS once per work-group and shared by the 4 waves; the next tile's
-//    global loads are in flight while the current one is computed.
+//  * A work-group (4 waves) owns one (sequence b, query head h, block of 128
+//    query rows); wave w owns 32 of those rows, one MFMA n-tile.  The kernel
+//    is sized for two work-groups per CU (<= 256 registers per lane, 68 KB of
+//    LDS), so every SIMD holds two waves and one wave's softmax arithmetic
+//    overlaps the other's matrix work.
+//  * Key tiles (64 keys for D <= 128, 32 for D = 256) are gathered from the
+//    paged pool (block table -> page -> row, 64-bit offsets) straight into
+//    LDS with global_load_lds_dwordx4: no registers or VALU stores on the way,
+//    and the next tile's loads are in flight while the current one is used.
+//    Rows are XOR-swizzled in 16-byte chunks (the swizzle is applied on the
+//    global side, since a wave's direct load fills 1 KB of LDS in lane order).
 //  * Scores are computed transposed, S^T = K . Q^T: K rows are the MFMA A
-//    operand read straight from LDS (16 contiguous bytes per lane) and the
-//    wave's Q rows are the B operand, held in registers for the whole loop.
-//    In the S^T accumulator layout each lane holds 4 consecutive keys of one
-//    query column, which is exactly the layout the B operand of the
-//    following O^T += V^T . P^T product needs -- the probabilities never
-//    leave registers, and the O^T rescale by the per-query correction is a
-//    per-lane multiply (the reference round-trips O through shared memory for
-//    it, kernels/paged_attn_wmma.cu:167-181).
-//  * V is stored transposed in LDS ([D][keys]) so the V^T A operand is two
-//    8-byte LDS reads per MFMA.
-//  * Causal work skipping: a work-group stops at the last key its last query
-//    row can see; a wave skips tiles beyond its own rows; masking is applied
-//    only on tiles that cross a wave's diagonal.
+//    operand read from LDS (16 bytes per lane), the wave's 32 query rows are
+//    the B operand held in registers for the whole loop.  In the 32x32 S^T
+//    accumulator layout a lane holds 16 keys of one query column, eight of
+//    which are exactly the B operand slots of one 16-key step of
+//    O^T += V^T . P^T -- probabilities never leave registers.  The V^T A
+//    operand is two ds_read_b64_tr_b16 per step.
+//  * The softmax is done in log2 units with the scale folded into one FMA per
+//    score; the running max is only raised when a tile's max exceeds it by
+//    more than 2^8 (probabilities stay <= 256, exact in fp16/bf16 range), so
+//    the O^T rescale is a rare wave-uniform branch instead of a per-tile
+//    multiply.  Masking runs only on tiles that cross a wave's diagonal.
 //  * Work-groups are ordered longest-first within a (sequence, head) and the
 //    (sequence, head) ranges are laid out so that consecutive ranges land on
 //    the same XCD (work-group i runs on XCD i mod 8), keeping a head's K/V
@@ -30,36 +34,63 @@
 // Semantics follow kernels/paged_attn_wmma.cu:80-205: query row r of the
 // chunk sits at ctx - S + r and sees keys [0, ctx - S + r]; accumulation and
 // the softmax are fp32; a row that sees no key is written as zeros (:200).
-// Precision: fp16 carries P and Q as the reference does (one rounding to
-// fp16, 11-bit significand).  bf16 has an 8-bit significand, too coarse for
-// the fp32-oracle tolerance, so P is carried as a bf16 hi + lo pair (two
-// P.V products, ~16-bit significand), and Q likewise whenever it does not
-// arrive in the KV type.
+// Precision: P is carried in fp16 (11-bit significand) as the reference does.
+// A bf16 V tile is converted to fp16 while it is staged, so P.V runs in fp16
+// too; if any staged |v| reaches 65520 (fp16 overflow, or inf) the
+// work-group restarts in a mode that keeps V in bf16 and carries P as a bf16
+// hi + lo pair (two P.V products, ~16-bit significand).  q that does not
+// arrive in the KV type is likewise split into hi + lo for Q.K^T.
 #include "pa_device.hpp"
 
 namespace pa {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef uint64_t u64x2_t __attribute__((ext_vector_type(2)));
 
-template <typename KV>
-__device__ inline float4_t mfma16x16x32(const u32x4_t& a, const u32x4_t& b, const float4_t& c) {
-  if constexpr (KV::kCode == kF16) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
-                                                  __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4):
+// lane i writes lds + 16*i; lds must be wave-uniform.  (A function of its own:
+// used directly in the kernel template, the builtin stops the host pass from
+// emitting the launch stubs.)
+__device__ inline void lds_dma16(const void* g, lds_void_t* lds) {
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
+template <bool kBf16>
+__device__ inline f32x16_t mfma32(const u32x4_t& a, const u32x4_t& b, const f32x16_t& c) {
+  if constexpr (kBf16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a),
+                                                  __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
   }
 }
 
-// fp32 -> 16-bit KV element bits, round to nearest even.
-template <typename KV>
-__device__ inline uint32_t to_bits16(float x) {
-  if constexpr (KV::kCode == kF16) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+// Two fp32 values -> one packed 16-bit pair, round to nearest even.
+template <bool kBf16>
+__device__ inline uint32_t pack2(float x, float y) {
+  if constexpr (kBf16) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{x, y}, bf16x2_t));
   } else {
-    return (uint32_t)f32_to_bf16_bits(x);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{x, y}, half2_t));
+  }
+}
+
+// The two fp32 values of a packed 16-bit pair.
+template <bool kBf16>
+__device__ inline float2_t unpack2(uint32_t w) {
+  if constexpr (kBf16) {
+    return float2_t{__builtin_bit_cast(float, w << 16), __builtin_bit_cast(float, w & 0xffff0000u)};
+  } else {
+    const half2_t h = __builtin_bit_cast(half2_t, w);
+    return float2_t{(float)h[0], (float)h[1]};
   }
 }
 
@@ -83,65 +114,85 @@ __device__ inline void load8f(const void* q, int dtype, int64_t idx, float (&x)[
   }
 }
 
-template <typename KV>
-__device__ inline float from_bits16(uint32_t h) {
-  if constexpr (KV::kCode == kF16) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
-  } else {
-    return __builtin_bit_cast(float, h << 16);
-  }
-}
-
-typedef short short4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) short4_t lds_short4_t;
-
-constexpr int kPfThreads = 256;  // 4 waves
+constexpr int kPfThreads = 256;   // 4 waves
 constexpr int kPfBtStage = 1024;  // block-table entries staged in LDS
+constexpr float kLazyRescale = 8.0f;  // raise the running max only past 2^8
 
-// Query rows per wave for head dims up to 128 (compile-time knob): 32 gives
-// each LDS K/V fragment two uses, 16 halves the registers.
-#ifndef PA_PF_QW
-#define PA_PF_QW 32
-#endif
+// How a tile's P.V product is formed.
+enum PvMode : int {
+  kPvDirect = 0,   // V tile loaded straight into LDS; P and V in fp16
+  kPvConvert = 1,  // bf16 V converted to fp16 while staged; P and V in fp16
+  kPvSplit = 2,    // bf16 V in LDS; P as bf16 hi + lo, two products
+};
+template <int M>
+struct PvTag {
+  static constexpr int value = M;
+};
 
 template <int D>
 struct PfShape {
-  static constexpr int QW = D <= 128 ? PA_PF_QW : 16;  // query rows per wave
-  static constexpr int NT = QW / 16;             // 16-column n-tiles per wave
+  static constexpr int QW = 32;                  // query rows per wave (one MFMA n-tile)
   static constexpr int QB = 4 * QW;              // query rows per work-group
   static constexpr int KB = D <= 128 ? 64 : 32;  // keys per tile
-  static constexpr int MT = KB / 16;             // 16-key m-tiles per tile
-  static constexpr int NSLAB = D / 32;           // 32-wide k-slabs of Q.K^T
-  static constexpr int NDT = D / 16;             // 16-row tiles of O^T
+  static constexpr int MT = KB / 32;             // 32-key m-tiles of S^T
+  static constexpr int KS = D / 16;              // 16-dim k-steps of Q.K^T
+  static constexpr int DT = D / 32;              // 32-dim m-tiles of O^T
   static constexpr int NCH = D / 8;              // 16-byte chunks per row
-  static constexpr int SWZ = NCH >= 8 ? 7 : NCH - 1;  // chunk swizzle mask
+  // LDS chunk swizzles (chunk cc of row r sits at position cc ^ f(r)), one per
+  // read pattern, so that every 256-byte LDS pass hits 64 distinct banks:
+  //  K, read as the S^T A operand (16 consecutive rows, one chunk):
+  //    f(r) = (r >> KSH) & KSW;
+  //  V, read transposed (4 consecutive rows x 4 consecutive chunks per 32
+  //  lanes): f(r) = ((r >> VSH) & VSW) << 2.
+  static constexpr int KSW = (NCH < 16 ? NCH : 16) - 1;
+  static constexpr int KSH = NCH >= 16 ? 0 : NCH == 8 ? 1 : 2;
+  static constexpr int VSW = NCH >= 16 ? 3 : NCH == 8 ? 1 : 0;
+  static constexpr int VSH = NCH >= 16 ? 0 : 1;
   static constexpr int CPT = KB * NCH / kPfThreads;    // chunks per thread per tile
+  static constexpr int WAVES_PER_EU = D <= 128 ? 2 : 1;
   static_assert(KB * NCH % kPfThreads == 0, "tile chunks must divide the work-group");
 };
 
-// LDS element offset of (row, chunk cc) in a swizzled [KB][D] tile: chunk cc of
-// row r lives at chunk position cc ^ (r & SWZ), which spreads the 16-byte
-// reads of 16 consecutive rows (same cc) over distinct banks.
+// LDS element offsets of (row, chunk cc) in the swizzled [KB][D] K and V tiles.
 template <int D>
-__device__ inline int swz(int row, int cc) {
-  return row * D + ((cc ^ (row & PfShape<D>::SWZ)) << 3);
+__device__ inline int kpos(int row, int cc) {
+  return cc ^ ((row >> PfShape<D>::KSH) & PfShape<D>::KSW);
+}
+template <int D>
+__device__ inline int vpos(int row, int cc) {
+  return cc ^ (((row >> PfShape<D>::VSH) & PfShape<D>::VSW) << 2);
+}
+template <int D>
+__device__ inline int swk(int row, int cc) {
+  return row * D + (kpos<D>(row, cc) << 3);
+}
+template <int D>
+__device__ inline int swv(int row, int cc) {
+  return row * D + (vpos<D>(row, cc) << 3);
 }
 
 template <typename KV, int D, bool kSplitQ>
-__global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillParams p) {
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(PfShape<D>::WAVES_PER_EU)))
+void prefill_mfma_kernel(const PrefillParams p) {
   using Sh = PfShape<D>;
-  constexpr int QW = Sh::QW, NT = Sh::NT, QB = Sh::QB, KB = Sh::KB, MT = Sh::MT;
-  constexpr int NSLAB = Sh::NSLAB, NDT = Sh::NDT, NCH = Sh::NCH, CPT = Sh::CPT;
+  constexpr int QW = Sh::QW, QB = Sh::QB, KB = Sh::KB, MT = Sh::MT, KS = Sh::KS, DT = Sh::DT;
+  constexpr int NCH = Sh::NCH, CPT = Sh::CPT;
+  constexpr bool kBf16 = KV::kCode == kBF16;
 
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][KB * D];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][KB * D];
-  __shared__ int s_badkey;  // first key whose page has an invalid block id
-  __shared__ int32_t s_bt[kPfBtStage];  // the work-group's block ids, when they fit
+  __shared__ __attribute__((aligned(16))) uint16_t sK0[KB * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sK1[KB * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sV0[KB * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sV1[KB * D];
+  __shared__ int32_t s_bt[kPfBtStage];  // window of the work-group's block ids
+  __shared__ int s_badkey;              // first key whose page has an invalid block id
+  __shared__ u64x2_t s_off0[KB];        // per-row K/V byte offsets of a tile (even / odd tiles)
+  __shared__ u64x2_t s_off1[KB];
+  __shared__ int s_ovf;                 // the fp16 pass produced a non-finite O
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int col = lane & 15;  // query column (S^T / O^T) or key row (K operand)
-  const int kg = lane >> 4;   // lane group: k-index block of the operands
+  const int n = lane & 31;   // query column of this lane (S^T, O^T) / key row (K operand)
+  const int hh = lane >> 5;  // lane half: k-slot block of the operands
 
   // Work-group -> (b, h, query block): XCD-contiguous, longest block first.
   const int nq = p.q_tiles;
@@ -158,291 +209,388 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   const int maxctx = p.MB * p.BS;
   const int qs0 = qt * QB;
   const int qw0 = qs0 + wave * QW;  // this wave's first query row
+  const int qrow = qw0 + n;
+  const bool live = qrow < p.S;
 
   if (ctx > maxctx) {  // context longer than the block table: poison rows that attend keys
-    for (int nt = 0; nt < NT; ++nt) {
-      const int qrow = qw0 + nt * 16 + col;
-      if (qrow < p.S && kg == 0) {
-        const float fillv = ctx - p.S + qrow < 0 ? 0.0f : __builtin_nanf("");
-        const int64_t orow = (((int64_t)b * p.S + qrow) * p.H + h) * D;
-        for (int d = 0; d < D; ++d) store_elem(p.out, p.out_dtype, orow + d, fillv);
-      }
+    if (live && hh == 0) {
+      const float fillv = ctx - p.S + qrow < 0 ? 0.0f : __builtin_nanf("");
+      const int64_t orow = (((int64_t)b * p.S + qrow) * p.H + h) * D;
+      for (int d = 0; d < D; ++d) store_elem(p.out, p.out_dtype, orow + d, fillv);
     }
     return;
   }
-  if (threadIdx.x == 0) s_badkey = 0x7fffffff;
+  if (threadIdx.x == 0) {
+    s_badkey = 0x7fffffff;
+    s_ovf = 0;
+  }
 
   // Keys the work-group's rows can see: [0, kend); this wave's rows: [0, wave_kend).
   const int kend = min(ctx, ctx - p.S + min(qs0 + QB, p.S));
   const int ntiles = kend > 0 ? (kend + KB - 1) / KB : 0;
   const int wave_last = min(qw0 + QW - 1, p.S - 1);
-  const int wave_kend = min(ctx, ctx - p.S + wave_last + 1);
-  const int wave_kfull = ctx - p.S + qw0 + 1;  // keys below this are visible to every row
-  const bool wave_padded = qw0 + QW > p.S;
+  const int wave_kend = qw0 < p.S ? min(ctx, ctx - p.S + wave_last + 1) : 0;
+  const int wave_kfull = ctx - p.S + qw0 + 1;  // keys below this are visible to every row of the wave
+  const int qpos = ctx - p.S + qrow;
+  const int qlim = min(qpos, kend - 1);        // last key this column may see
 
-  // Q^T operands (rows qw0 + nt*16 + col, dims c*32 + kg*8 .. +8), rounded to
-  // the KV type, with the rounding residual for the low-part product.
-  u32x4_t qf[NT][NSLAB], qf_lo[kSplitQ ? NT : 1][NSLAB];
-  int qpos[NT];
-  bool live[NT];
+  // Q^T operand (row qrow, dims ks*16 + hh*8 .. +8) in the KV type.  The sign of
+  // the scale is applied here (exactly), so the softmax scale below is positive.
+  u32x4_t qf[KS], qf_lo[kSplitQ ? KS : 1];
+  {
+    const int64_t qoff = (((int64_t)b * p.S + (live ? qrow : 0)) * p.H + h) * D + hh * 8;
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int qrow = qw0 + nt * 16 + col;
-    live[nt] = qrow < p.S;
-    qpos[nt] = ctx - p.S + qrow;
-    const int64_t qrow_off = (((int64_t)b * p.S + qrow) * p.H + h) * D;
-#pragma unroll
-    for (int c = 0; c < NSLAB; ++c) {
-      uint32_t w[4], wl[4];
-      float xv[8];
-      if (live[nt]) {
-        load8f(p.q, p.q_dtype, qrow_off + c * 32 + kg * 8, xv);
+    for (int ks = 0; ks < KS; ++ks) {
+      if constexpr (!kSplitQ) {
+        u32x4_t r = u32x4_t{0u, 0u, 0u, 0u};
+        if (live) r = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p.q) + qoff + ks * 16);
+        qf[ks] = (r & p.q_and) ^ p.q_xor;
       } else {
+        float xv[8];
+        if (live) {
+          load8f(p.q, p.q_dtype, qoff + ks * 16, xv);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xv[e] = 0.0f;
-      }
+          for (int e = 0; e < 8; ++e) xv[e] = 0.0f;
+        }
+        uint32_t w[4], wl[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float x0 = xv[2 * j], x1 = xv[2 * j + 1];
-        const uint32_t h0 = to_bits16<KV>(x0), h1 = to_bits16<KV>(x1);
-        w[j] = h0 | (h1 << 16);
-        wl[j] = to_bits16<KV>(x0 - from_bits16<KV>(h0)) | (to_bits16<KV>(x1 - from_bits16<KV>(h1)) << 16);
+        for (int j = 0; j < 4; ++j) {
+          const float x0 = xv[2 * j] * p.q_sign, x1 = xv[2 * j + 1] * p.q_sign;
+          w[j] = pack2<kBf16>(x0, x1);
+          const float2_t r = unpack2<kBf16>(w[j]);
+          wl[j] = pack2<kBf16>(x0 - r[0], x1 - r[1]);
+        }
+        qf[ks] = u32x4_t{w[0], w[1], w[2], w[3]};
+        qf_lo[ks] = u32x4_t{wl[0], wl[1], wl[2], wl[3]};
       }
-      qf[nt][c] = u32x4_t{w[0], w[1], w[2], w[3]};
-      if constexpr (kSplitQ) qf_lo[nt][c] = u32x4_t{wl[0], wl[1], wl[2], wl[3]};
     }
   }
-  constexpr bool kSplitP = KV::kCode == kBF16;
-
-  float4_t o[NDT][NT];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) o[dt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m[NT], l[NT];  // l: this lane group's share of the row sum
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    m[nt] = kNegBig;
-    l[nt] = 0.0f;
-  }
+  const float qscale = p.qscale;
 
   const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
   // Block ids of the pages this work-group reads live in an LDS window of
-  // kPfBtStage pages starting at page win0, so a tile's K/V loads never wait
+  // kPfBtStage pages starting at page win0, so a tile's loads never wait
   // behind a dependent block-table load.  The window moves (at a tile
-  // boundary, behind a barrier) when the next tile to load leaves it.
+  // boundary, between barriers) when the next tile to load leaves it.
   const int npages = kend > 0 ? (int)fastdiv((uint32_t)(kend - 1), p.bs_div) + 1 : 0;
   int win0 = 0;
   auto stage = [&](int first) {
     win0 = first;
-    const int n = min(kPfBtStage, npages - first);
-    for (int i = threadIdx.x; i < n; i += kPfThreads) s_bt[i] = bt_row[first + i];
+    const int cnt = min(kPfBtStage, npages - first);
+    for (int i = threadIdx.x; i < cnt; i += kPfThreads) s_bt[i] = bt_row[first + i];
   };
-  auto ensure_window = [&](int t) {  // uniform; call with every thread, then barrier
+  auto ensure_window = [&](int t) {  // work-group uniform
     const int last = min(t * KB + KB, kend) - 1;
     const int plast = (int)fastdiv((uint32_t)last, p.bs_div);
     if (plast >= win0 + kPfBtStage) {
-      __syncthreads();  // every gload of the old window is done
+      __syncthreads();
       stage((int)fastdiv((uint32_t)(t * KB), p.bs_div));
       __syncthreads();
     }
   };
-  stage(0);
-  __syncthreads();
-  const int64_t k_sb = p.k_sb * 2, k_st = p.k_st * 2, k_sh = (int64_t)kvh * p.k_sh * 2;
-  const int64_t v_sb = p.v_sb * 2, v_st = p.v_st * 2, v_sh = (int64_t)kvh * p.v_sh * 2;
+
+  const char* kbase = static_cast<const char*>(p.k) + (int64_t)kvh * p.k_sh * 2;
+  const char* vbase = static_cast<const char*>(p.v) + (int64_t)kvh * p.v_sh * 2;
+  const uint32_t k_sbb = (uint32_t)(p.k_sb * 2), k_stb = (uint32_t)(p.k_st * 2);
+  const uint32_t v_sbb = (uint32_t)(p.v_sb * 2), v_stb = (uint32_t)(p.v_st * 2);
   const uint64_t nb = (uint64_t)p.num_blocks;
+
+  // This thread's chunks of a tile: chunk c fills LDS chunk position
+  // pos = (c*4 + wave)*64 + lane (wave-contiguous 1 KB per direct load), i.e.
+  // row pos / NCH at swizzled position pos % NCH; it loads the source chunk
+  // whose swizzled position that is (an involution: the same XOR).
+  int prow[CPT], ksrc[CPT], vsrc[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int pos = (c * 4 + wave) * 64 + lane;
+    prow[c] = pos / NCH;
+    ksrc[c] = kpos<D>(prow[c], pos % NCH) * 16;
+    vsrc[c] = vpos<D>(prow[c], pos % NCH) * 16;
+  }
   int badkey = 0x7fffffff;
 
-  // Global -> registers for tile t (16-byte chunks), registers -> LDS (swizzled).
-  // Global -> registers for tile t.  Branch-free: a row past kend, or on a
-  // page with an invalid block id, loads row 0 of block 0 (in bounds, NB >= 1)
-  // and is zeroed when stored to LDS.
-  u32x4_t rk[CPT], rv[CPT];
-  uint32_t rmask = 0;
-  const char* kbase = static_cast<const char*>(p.k) + k_sh;
-  const char* vbase = static_cast<const char*>(p.v) + v_sh;
-  auto gload = [&](int t) {
-    int blk[CPT], off[CPT];
-    bool val[CPT];
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int idx = (int)threadIdx.x + c * kPfThreads;
-      const int row = idx / NCH;
-      const int kabs = t * KB + row;
-      val[c] = kabs < kend;
-      const int pg = (int)fastdiv((uint32_t)(val[c] ? kabs : 0), p.bs_div);
-      off[c] = (val[c] ? kabs : 0) - pg * p.BS;
-      blk[c] = s_bt[val[c] ? pg - win0 : 0];
-    }
-    uint32_t mask = 0;
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int idx = (int)threadIdx.x + c * kPfThreads;
-      const int cc = idx - (idx / NCH) * NCH;
-      const bool okb = (uint64_t)(int64_t)blk[c] < nb;
-      if (val[c] && !okb) badkey = min(badkey, t * KB + idx / NCH);
-      const bool use = val[c] && okb;
-      const int64_t bb = use ? blk[c] : 0;
-      const int64_t oo = use ? off[c] : 0;
-      rk[c] = load16(kbase, bb * k_sb + oo * k_st + cc * 16);
-      rv[c] = load16(vbase, bb * v_sb + oo * v_st + cc * 16);
-      mask |= use ? (1u << c) : 0u;
-    }
-    rmask = mask;
-  };
-  auto sstore = [&](int buf) {
-    const u32x4_t zero = u32x4_t{0, 0, 0, 0};
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int idx = (int)threadIdx.x + c * kPfThreads;
-      const int row = idx / NCH, cc = idx - (idx / NCH) * NCH;
-      const bool use = (rmask >> c) & 1u;
-      *reinterpret_cast<u32x4_t*>(&sK[buf][swz<D>(row, cc)]) = use ? rk[c] : zero;
-      *reinterpret_cast<u32x4_t*>(&sV[buf][swz<D>(row, cc)]) = use ? rv[c] : zero;
+  // Row offsets of a tile, built once per tile by wave 0 (one row per lane)
+  // two tiles ahead, so the other waves' loads cost one LDS read and an add
+  // per chunk.  Entry r = {K byte offset, V byte offset | use}; a row past
+  // kend, or on a page with an invalid block id, points at row 0 of block 0
+  // (in bounds, NB >= 1) with use = 0.  Offsets are multiples of 16 bytes, so
+  // bit 0 of the V offset is free for the flag.
+  auto build = [&](int t, u64x2_t* tb) {
+    if (wave == 0 && lane < KB) {
+      const int kabs = t * KB + lane;
+      const bool valid = kabs < kend;
+      const int kk = valid ? kabs : 0;
+      const int pg = (int)fastdiv((uint32_t)kk, p.bs_div);
+      const int off = kk - pg * p.BS;
+      const int blk = s_bt[valid ? pg - win0 : 0];
+      const bool okb = (uint64_t)(int64_t)blk < nb;
+      if (valid && !okb) badkey = min(badkey, kabs);
+      const bool use = valid && okb;
+      const uint32_t ub = use ? (uint32_t)blk : 0u, uo = use ? (uint32_t)off : 0u;
+      tb[lane] = u64x2_t{(uint64_t)ub * k_sbb + uo * k_stb,
+                         ((uint64_t)ub * v_sbb + uo * v_stb) | (use ? 1u : 0u)};
     }
   };
 
-  auto compute = [&](int t, int buf) {
-    const int tk0 = t * KB;
-    // S^T = K . Q^T: MT x NT tiles of 16 keys x 16 queries.
-    float4_t st[MT][NT];
+  f32x16_t o[DT];
+  float m = -__builtin_inff(), l = 0.0f;  // running max (log2 units); this lane half's row sum
+
+  // One pass over the key tiles in PV mode kMode.  Returns false (work-group
+  // uniform) when kPvConvert produced a non-finite O (a V value that fp16
+  // cannot hold, or non-finite data): the caller reruns in kPvSplit.
+  auto run = [&](auto mode_tag) -> bool {
+    constexpr int kMode = decltype(mode_tag)::value;
+    constexpr bool kDirectV = kMode != kPvConvert;
+    constexpr bool kPvBf16 = kMode == kPvSplit;
+
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
+    for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) st[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+      for (int r = 0; r < 16; ++r) o[dt][r] = 0.0f;
+    }
+    m = -__builtin_inff();
+    l = 0.0f;
+
+    u32x4_t vreg[kDirectV ? 1 : CPT];
+    uint32_t umask = 0;
+
+    // Loads of a tile into (dK, dV) from its offset table: entries() reads
+    // this thread's table entries, chunk(c) issues chunk c's K (and V unless
+    // converted) loads straight to LDS.
+    u64x2_t ent[CPT];
+    auto entries = [&](const u64x2_t* tb) {
 #pragma unroll
-      for (int c = 0; c < NSLAB; ++c) {
-        const int row = mt * 16 + col;
-        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&sK[buf][swz<D>(row, c * 4 + kg)]);
+      for (int c = 0; c < CPT; ++c) ent[c] = tb[prow[c]];
+      umask = 0;
+    };
+    auto chunk = [&](int c, uint16_t* dK, uint16_t* dV) {
+      const uint32_t use = (uint32_t)ent[c][1] & 1u;
+      umask |= use << c;
+      lds_dma16(kbase + ent[c][0] + ksrc[c], (lds_void_t*)(dK + (c * 4 + wave) * 512));
+      const char* va = vbase + (ent[c][1] - use) + vsrc[c];
+      if constexpr (kDirectV) {
+        lds_dma16(va, (lds_void_t*)(dV + (c * 4 + wave) * 512));
+      } else {
+        vreg[c] = *reinterpret_cast<const u32x4_t*>(va);
+      }
+    };
+    auto issue = [&](const u64x2_t* tb, uint16_t* dK, uint16_t* dV) {
+      entries(tb);
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          st[mt][nt] = mfma16x16x32<KV>(a, qf[nt][c], st[mt][nt]);
-          if constexpr (kSplitQ) st[mt][nt] = mfma16x16x32<KV>(a, qf_lo[nt][c], st[mt][nt]);
+      for (int c = 0; c < CPT; ++c) chunk(c, dK, dV);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // After a tile's loads are complete: zero V rows that were substituted
+    // (their probabilities are 0, but substituted data may not be finite),
+    // or convert the register-staged bf16 V to fp16 (exact for
+    // 2^-17 <= |v| < 65504; smaller values round to fp16 subnormals).
+    auto finish = [&](uint16_t* dV) {
+      if constexpr (kDirectV) {
+        if (umask != (1u << CPT) - 1u) {
+#pragma unroll
+          for (int c = 0; c < CPT; ++c) {
+            if (!((umask >> c) & 1u))
+              *reinterpret_cast<u32x4_t*>(dV + ((c * 4 + wave) * 64 + lane) * 8) = u32x4_t{0u, 0u, 0u, 0u};
+          }
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+          const bool use = (umask >> c) & 1u;
+          u32x4_t w;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t x = vreg[c][j];
+            w[j] = pack2<false>(__builtin_bit_cast(float, x << 16), __builtin_bit_cast(float, x & 0xffff0000u));
+          }
+          if (!use) w = u32x4_t{0u, 0u, 0u, 0u};
+          *reinterpret_cast<u32x4_t*>(dV + ((c * 4 + wave) * 64 + lane) * 8) = w;
         }
       }
-    }
-    // Online softmax per query column; keys of this lane: tk0 + mt*16 + kg*4 + i.
-    const bool need_mask = tk0 + KB > wave_kfull || wave_padded;
-    u32x4_t pb[KB / 32][NT], pb_lo[KB / 32][NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      float mx = kNegBig;
+    };
+
+    // S^T, softmax and O^T update for tile t from LDS (cK, cV).
+    auto compute = [&](int t, const uint16_t* cK, const uint16_t* cV) {
+      f32x16_t st[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float sv = st[mt][nt][i] * p.qscale;
-          if (need_mask) {
-            const int key = tk0 + mt * 16 + kg * 4 + i;
-            if (!(live[nt] && key <= qpos[nt])) sv = kNegBig;
-          }
-          st[mt][nt][i] = sv;
-          mx = fmaxf(mx, sv);
+        for (int r = 0; r < 16; ++r) st[mt][r] = 0.0f;
+      }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const u32x4_t a = *reinterpret_cast<const u32x4_t*>(cK + swk<D>(mt * 32 + n, 2 * ks + hh));
+          st[mt] = mfma32<kBf16>(a, qf[ks], st[mt]);
+          if constexpr (kSplitQ) st[mt] = mfma32<kBf16>(a, qf_lo[ks], st[mt]);
         }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mn = fmaxf(m[nt], mx);
-      const float corr = fast_exp2(m[nt] - mn);
-      m[nt] = mn;
-      float ls = l[nt] * corr;
+      // Keys of this lane: t*KB + mt*32 + 8*(r/4) + 4*hh + r%4.  Only tiles
+      // that cross the wave's diagonal (or the end of the keys) are masked;
+      // the empty asm keeps this a branch rather than selects on every tile.
+      const int tk0 = t * KB;
+      if (tk0 + KB > wave_kfull) {
+        asm volatile("");
+        const int thr = qlim - tk0 - 4 * hh;
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) o[dt][nt] *= corr;
-      // P^T operand per 32-key chunk c2: keys c2*32 + kg*4 + {0..3} (m-tile 2*c2)
-      // then c2*32 + 16 + kg*4 + {0..3} (m-tile 2*c2+1), matching the V^T reads.
+        for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-      for (int c2 = 0; c2 < KB / 32; ++c2) {
-        uint32_t w[4], wl[4];
+          for (int r = 0; r < 16; ++r) {
+            if (mt * 32 + 8 * (r >> 2) + (r & 3) > thr) st[mt][r] = -__builtin_inff();
+          }
+        }
+      }
+      float mx = -__builtin_inff();
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
+      for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const float s0 = st[2 * c2 + half][nt][2 * j];
-            const float s1 = st[2 * c2 + half][nt][2 * j + 1];
-            const float p0 = s0 > kNegBig ? fast_exp2(s0 - mn) : 0.0f;
-            const float p1 = s1 > kNegBig ? fast_exp2(s1 - mn) : 0.0f;
-            const uint32_t h0 = to_bits16<KV>(p0), h1 = to_bits16<KV>(p1);
-            w[half * 2 + j] = h0 | (h1 << 16);
-            if constexpr (kSplitP) {
-              ls += p0 + p1;
-              wl[half * 2 + j] = to_bits16<KV>(p0 - from_bits16<KV>(h0)) |
-                                 (to_bits16<KV>(p1 - from_bits16<KV>(h1)) << 16);
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // the other half holds the column's other keys
+      const float mxs = mx * qscale;
+      if (__builtin_amdgcn_ballot_w64(mxs > m + kLazyRescale) != 0) {
+        asm volatile("");  // rare: keep the O^T rescale behind the branch
+        const float mn = fmaxf(m, mxs);
+        const float corr = mn == -__builtin_inff() ? 1.0f : fast_exp2(m - mn);
+        m = mn;
+        l *= corr;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;
+      }
+      const float negm = m == -__builtin_inff() ? 0.0f : -m;
+
+      // Per 32-key m-tile: P^T operands of its two 16-key steps (accumulator
+      // slots 8s .. 8s+7 of step s), then O^T += V^T . P^T.  V^T operand of
+      // step (mt, s): lane l of 16-lane group g supplies row
+      // mt*32 + 16s + 4*hh + (l%16)/4 (and +8), dims dt*32 + 16*(g%2) +
+      // (l%4)*4 .. +4, and receives dim dt*32 + lane%32.
+      const int li = lane & 15;
+      const int trow = 4 * hh + (li >> 2);
+      const int tcol = 16 * ((lane >> 4) & 1) + (li & 3) * 4;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        u32x4_t pb[2], pb_lo[kPvBf16 ? 2 : 1];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          uint32_t w[4], wl[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float p0 = fast_exp2(fmaf(st[mt][8 * s + 2 * j], qscale, negm));
+            const float p1 = fast_exp2(fmaf(st[mt][8 * s + 2 * j + 1], qscale, negm));
+            w[j] = pack2<kPvBf16>(p0, p1);
+            if constexpr (kPvBf16) {
+              const float2_t r = unpack2<true>(w[j]);
+              wl[j] = pack2<true>(p0 - r[0], p1 - r[1]);
+              l += p0 + p1;
             } else {
-              ls += from_bits16<KV>(h0) + from_bits16<KV>(h1);
+              l = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w[j]), half2_t{1.0f16, 1.0f16}, l, false);
             }
           }
+          pb[s] = u32x4_t{w[0], w[1], w[2], w[3]};
+          if constexpr (kPvBf16) pb_lo[s] = u32x4_t{wl[0], wl[1], wl[2], wl[3]};
         }
-        pb[c2][nt] = u32x4_t{w[0], w[1], w[2], w[3]};
-        if constexpr (kSplitP) pb_lo[c2][nt] = u32x4_t{wl[0], wl[1], wl[2], wl[3]};
-      }
-      l[nt] = ls;
-    }
-    // O^T += V^T . P^T.  V^T operand for (c2, dt): two transposing 8-byte LDS
-    // reads; lane j of each 16-lane group supplies row key_base + j/4, dims
-    // dt*16 + (j%4)*4 .. +4, and receives dim dt*16 + j for the 4 rows.
-    const int trow = col >> 2, tcol = (col & 3) * 4;
 #pragma unroll
-    for (int c2 = 0; c2 < KB / 32; ++c2) {
+        for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const int r0 = c2 * 32 + kg * 4 + trow;
-        const int r1 = r0 + 16;
-        const int dcol = dt * 16 + tcol;
-        const int e0 = swz<D>(r0, dcol >> 3) + (dcol & 7);
-        const int e1 = swz<D>(r1, dcol >> 3) + (dcol & 7);
-        const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(&sV[buf][e0]));
-        const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(&sV[buf][e1]));
-        const uint64_t lo64 = __builtin_bit_cast(uint64_t, lo), hi64 = __builtin_bit_cast(uint64_t, hi);
-        const u32x4_t a = u32x4_t{(uint32_t)lo64, (uint32_t)(lo64 >> 32), (uint32_t)hi64,
-                                  (uint32_t)(hi64 >> 32)};
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          o[dt][nt] = mfma16x16x32<KV>(a, pb[c2][nt], o[dt][nt]);
-          if constexpr (kSplitP) o[dt][nt] = mfma16x16x32<KV>(a, pb_lo[c2][nt], o[dt][nt]);
+          for (int s = 0; s < 2; ++s) {
+            const int r0 = mt * 32 + 16 * s + trow;
+            const int col = dt * 32 + tcol;
+            const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_short4_t*)(cV + swv<D>(r0, col >> 3) + (col & 7)));
+            const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_short4_t*)(cV + swv<D>(r0 + 8, col >> 3) + (col & 7)));
+            const uint64_t lo64 = __builtin_bit_cast(uint64_t, lo), hi64 = __builtin_bit_cast(uint64_t, hi);
+            const u32x4_t a = u32x4_t{(uint32_t)lo64, (uint32_t)(lo64 >> 32), (uint32_t)hi64,
+                                      (uint32_t)(hi64 >> 32)};
+            o[dt] = mfma32<kPvBf16>(a, pb[s], o[dt]);
+            if constexpr (kPvBf16) o[dt] = mfma32<true>(a, pb_lo[s], o[dt]);
+          }
         }
       }
+    };
+
+    // Double-buffered tiles, unrolled by two so each LDS buffer (and offset
+    // table) is a distinct object: tile t+1's loads and tile t+2's offset
+    // table are produced while tile t is computed; one barrier per tile.
+    stage(0);
+    __syncthreads();
+    build(0, s_off0);
+    if (ntiles > 1) {
+      ensure_window(1);
+      build(1, s_off1);
     }
+    __syncthreads();
+    if (ntiles > 0) {
+      issue(s_off0, sK0, sV0);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's loads are in LDS
+      finish(sV0);
+    }
+    __syncthreads();
+    for (int t = 0; t < ntiles; t += 2) {
+      if (t + 2 < ntiles) ensure_window(t + 2);
+      if (t + 2 < ntiles) build(t + 2, s_off0);
+      const bool more1 = t + 1 < ntiles;
+      if (more1) issue(s_off1, sK1, sV1);
+      if (t * KB < wave_kend) compute(t, sK0, sV0);
+      if (more1) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        finish(sV1);
+      }
+      __syncthreads();
+      if (!more1) break;
+      if (t + 3 < ntiles) ensure_window(t + 3);
+      if (t + 3 < ntiles) build(t + 3, s_off1);
+      const bool more2 = t + 2 < ntiles;
+      if (more2) issue(s_off0, sK0, sV0);
+      if ((t + 1) * KB < wave_kend) compute(t + 1, sK1, sV1);
+      if (t + 2 < ntiles) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        finish(sV0);
+      }
+      __syncthreads();
+    }
+    if constexpr (kMode == kPvConvert) {
+      bool bad = false;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bad |= !__builtin_isfinite(o[dt][r]);
+      }
+      if (bad) s_ovf = 1;
+      __syncthreads();
+      if (s_ovf) return false;
+    }
+    return true;
   };
 
-  // Double-buffered tiles: the next tile's global loads are in flight while
-  // the current tile is computed; one barrier per tile.
-  if (ntiles > 0) {
-    gload(0);
-    sstore(0);
-  }
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) {
-      ensure_window(t + 1);
-      gload(t + 1);
+  if constexpr (kBf16) {
+    if (!run(PvTag<kPvConvert>{})) {
+      badkey = 0x7fffffff;
+      run(PvTag<kPvSplit>{});
     }
-    if (t * KB < wave_kend) compute(t, buf);
-    if (t + 1 < ntiles) sstore(buf ^ 1);
-    __syncthreads();
+  } else {
+    run(PvTag<kPvDirect>{});
   }
+
   if (badkey != 0x7fffffff) atomicMin(&s_badkey, badkey);
   __syncthreads();
   const int bad_from = s_badkey;
 
-  // Row sums over the 4 lane groups, normalise, write 4 dims per lane per O^T tile.
+  // Row sum over the two lane halves, normalise, write.  O^T slot r of lane
+  // (n, hh) in m-tile dt is dim dt*32 + 8*(r/4) + 4*hh + r%4 of row qrow.
+  const float lt = l + __shfl_xor(l, 32, 64);
+  if (!live) return;
+  const bool bad = bad_from <= qpos;
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  const int64_t orow = (((int64_t)b * p.S + qrow) * p.H + h) * D;
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    float lt = l[nt] + __shfl_xor(l[nt], 16, 64);
-    lt += __shfl_xor(lt, 32, 64);
-    if (!live[nt]) continue;
-    const bool bad = bad_from <= qpos[nt];
-    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-    const int qrow = qw0 + nt * 16 + col;
-    const int64_t orow = (((int64_t)b * p.S + qrow) * p.H + h) * D;
+  for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = dt * 16 + kg * 4 + i;
-        store_elem(p.out, p.out_dtype, orow + d, bad ? __builtin_nanf("") : o[dt][nt][i] * inv);
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int d = dt * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+      store_elem(p.out, p.out_dtype, orow + d, bad ? __builtin_nanf("") : o[dt][r] * inv);
     }
   }
 }

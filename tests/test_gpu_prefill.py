@@ -123,3 +123,31 @@ def test_prefill_bad_block_and_long_context(pa, dev):
         got = to_host(fn(q, k, v, torch.from_numpy(bt).to(dev), torch.from_numpy(ctx).to(dev), 0.1))
         assert np.array_equal(np.isnan(got), np.isnan(want))
         close(got, want)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_mfma_prefill_bf16_values_beyond_fp16(pa, dev, D):
+    """bf16 V values that fp16 cannot hold (|v| >= 65520) on a few keys, one of
+    them on the diagonal tile: rows that see them and rows that do not must
+    both match the oracle (the kernel redoes such work-groups with V in bf16)."""
+    S, BS = 200, 16
+    inp = prefill_case(2, S, 4, 2, D, BS, [S, S + 37], seed=D + 1, kv="bf16", qt="bf16")
+    v = inp["v"].copy()
+    for b, key, val in ((0, 100, 1.0e6), (0, 3, -7.0e4), (1, 150, 3.0e5)):
+        blk, row = inp["bt"][b, key // BS], key % BS
+        v[blk, row] = oracle.quantize(np.full(v.shape[2:], val, np.float32), "bf16")
+    inp["v"] = v
+    got = pa.paged_attention_prefill_wmma(*dev_args(inp, dev), 1.0 / np.sqrt(D))
+    want = want_of(inp, 1.0 / np.sqrt(D))
+    assert np.isfinite(want).all() and np.abs(want).max() > 1e3
+    close(to_host(got), want)
+
+
+@pytest.mark.parametrize("scale", [-0.15, 0.0])
+@pytest.mark.parametrize("kv,qt", [("f16", "f16"), ("bf16", "bf16"), ("f16", "f32")])
+def test_mfma_prefill_scale_sign(pa, dev, scale, kv, qt):
+    """A negative scale (the running max must follow the scaled scores) and a
+    zero scale (uniform weights over the visible keys)."""
+    inp = prefill_case(2, 90, 4, 4, 64, 16, [90, 130], seed=11, kv=kv, qt=qt)
+    got = pa.paged_attention_prefill_wmma(*dev_args(inp, dev), scale)
+    close(to_host(got), want_of(inp, scale))
