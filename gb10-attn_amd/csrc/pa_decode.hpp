@@ -1,7 +1,7 @@
 // pa_decode.hpp -- gfx950 paged-attention decode kernel (context-split pass).
 //
 // Work unit: one work-group (4 waves of 64 lanes) per
-//   (query row z, KV head kvh, head chunk hc, partition part).
+//   (query row z, partition part, KV head kvh, head chunk hc), heads fastest.
 // The GC query heads of one GQA group that share KV head kvh are served by
 // the same work-group, so every K/V page is read from HBM once per KV head
 // (the reference reads it once per query head, kernels/paged_attn_v3.cu:63).
@@ -79,13 +79,16 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodePara
   const int slot = lane / LPT;
   const int sub = lane % LPT;
 
-  // blockIdx.x -> (z, kvh, hc, part), partition fastest.
+  // blockIdx.x -> (z, part, kvh, hc), heads fastest: the work-groups that
+  // read the other heads' rows of the same pages are dispatched together, so
+  // a page's DRAM rows are open for all of them (one KV head's row of a token
+  // is a 128-256 byte slice of the page's token row).
   const int units_y = p.HKV * p.head_chunks;
   int id = blockIdx.x;
-  const int part = id % p.parts;
-  id /= p.parts;
   const int y = id % units_y;
-  const int z = id / units_y;
+  id /= units_y;
+  const int part = id % p.parts;
+  const int z = id / p.parts;
   const int kvh = y / p.head_chunks;
   const int hc = y - kvh * p.head_chunks;
   const int b = z / p.Sq;
