@@ -274,6 +274,49 @@ def cpu_baseline(work, seconds):
     }
 
 
+def simd_cpu(work, threads, seconds=2.0):
+    """Our SIMD/OpenMP port of cpu_reference (oracle/pa_oracle_simd.c, AVX2 + F16C),
+    parallel over (sequence, head) on `threads` host cores (BASELINE CPU path 2)."""
+    import oracle
+    nsamp = min(16, work.B)
+    bt = work.bt_host[:nsamp]
+    used = np.unique(bt[bt >= 0])
+    remap = np.full(work.k[0].shape[0], -1, np.int64)
+    remap[used] = np.arange(used.size)
+    idx = torch.from_numpy(used).to(work.k[0].device)
+    tag = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}[work.k[0].dtype]
+    as_np = (lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)) if tag == "bf16" else (lambda t: t.cpu().numpy())
+    k = np.ascontiguousarray(as_np(work.k[0][idx]))
+    v = np.ascontiguousarray(as_np(work.v[0][idx]))
+    bts = np.ascontiguousarray(remap[bt].astype(np.int32))
+    ctx = np.ascontiguousarray(work.ctx_host[:nsamp])
+    q = np.ascontiguousarray(work.q[:nsamp].float().cpu().numpy())
+    run = lambda: oracle.decode_simd(q, k, v, bts, ctx, work.scale, tag, threads=threads)
+    run()
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        run()
+        n += 1
+    el = time.perf_counter() - t0
+    sample_bytes = 2.0 * float(ctx.sum()) * work.HKV * work.D * work.k[0].element_size()
+    return {"value": round(sample_bytes * n / el / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port_simd_openmp",
+            "sample": f"{nsamp} sequences (all heads), {n} calls in {el:.1f} s; the same sample each call "
+                      f"(host-cache resident)"}
+
+
+def host_info():
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu": model, "nproc": os.cpu_count(), "threads_used": 16}
+
+
 def torch_sdpa_cpu(work, threads):
     """PyTorch SDPA on the gathered paged layout, on the host CPU (BASELINE CPU path 3)."""
     torch.set_num_threads(threads)
@@ -292,7 +335,8 @@ def torch_sdpa_cpu(work, threads):
     el = time.perf_counter() - t0
     sample_bytes = 2.0 * nsamp * float(work.ctx_host[0]) * work.HKV * work.D * work.k[0].element_size()
     return {"value": round(sample_bytes * n / el / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "torch_sdpa_gathered", "sample": f"{nsamp} sequences, {n} calls"}
+            "kind": "torch_sdpa_gathered",
+            "sample": f"{nsamp} sequences gathered to fp32, {n} calls; the same sample each call (host-cache resident)"}
 
 
 # --------------------------------------------------------------- workloads --
@@ -427,7 +471,8 @@ def main():
     }
     log("bench: cpu baseline (reference cpu_reference, 1 thread)")
     line["cpu_baseline"] = cpu_baseline(work, args.cpu_seconds)
-    line["cpu_extra"] = [torch_sdpa_cpu(work, 16)]
+    line["cpu_extra"] = [simd_cpu(work, 16), torch_sdpa_cpu(work, 16)]
+    line["host"] = host_info()
     del work
     torch.cuda.empty_cache()
 

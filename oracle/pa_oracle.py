@@ -18,6 +18,7 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "liboracle.so"
+SIMD_PATH = HERE / "liboracle_simd.so"
 REF_PATH = HERE / "_ref" / "libgb10_ref.so"
 
 DTYPE_CODE = {"f32": 0, "f16": 1, "bf16": 2, "f64": 3}
@@ -199,6 +200,33 @@ def decode(q, k, v, bt, ctx, scale, kv_dtype="f32", online=False) -> np.ndarray:
     out = np.empty((B, H, D), np.float32)
     fn = lib().oracle_decode_online if online else lib().oracle_decode
     fn(_p(out), _p(q), C.byref(kv), _p(bt), bts, _p(ctx), B, H, HKV, D, BS, MB, C.c_float(scale))
+    return out
+
+
+_simd = None
+
+
+def decode_simd(q, k, v, bt, ctx, scale, kv_dtype="f32", threads=None) -> np.ndarray:
+    """The SIMD/OpenMP CPU baseline (pa_oracle_simd.c): cpu_reference's algorithm,
+    parallel over (b, h), AVX2-vectorised over D.  kv_dtype f32 / f16 / bf16."""
+    global _simd
+    if _simd is None:
+        L = C.CDLL(str(SIMD_PATH))
+        P, I, I64 = C.c_void_p, C.c_int, C.c_int64
+        L.oracle_decode_simd.argtypes = [P, P, P, P, I, I64, I64, I64, P, I64, P] + [I] * 6 + [C.c_float, I]
+        L.oracle_decode_simd.restype = I
+        _simd = L
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    B, H, D = q.shape
+    assert k.dtype == NP_OF[kv_dtype] and k.strides == v.strides and k.strides[3] == k.itemsize
+    sb, st, sh = (x // k.itemsize for x in k.strides[:3])
+    bt, bts, ctx = _tables(bt, ctx)
+    out = np.empty((B, H, D), np.float32)
+    threads = threads or os.cpu_count()
+    rc = _simd.oracle_decode_simd(_p(out), _p(q), _p(k), _p(v), DTYPE_CODE[kv_dtype], sb, st, sh, _p(bt), bts,
+                                  _p(ctx), B, H, k.shape[2], D, k.shape[1], bt.shape[1], C.c_float(scale),
+                                  int(threads))
+    assert rc == 0
     return out
 
 

@@ -369,3 +369,14 @@ def test_dot_softmax_bit_exact_vs_arm_scalar():
         r = x.copy()
         oracle.ref().ref_softmax_inplace(_p(r), n)
         assert np.array_equal(oracle.softmax(x), r)
+
+
+@pytest.mark.parametrize("kv", ["f32", "f16", "bf16"])
+def test_simd_baseline_matches_scalar_oracle(kv):
+    """The SIMD/OpenMP CPU baseline computes cpu_reference's result (summation order
+    differs: fp32 rounding only), including GQA and an empty context."""
+    inp = oracle.paged_inputs(3, 8, 2, 64, 16, [70, 0, 33], seed=21, kv_dtype=kv)
+    want = oracle.decode(inp["q_f32"], inp["k"], inp["v"], inp["bt"], inp["ctx"], 0.125, kv)
+    got = oracle.decode_simd(inp["q_f32"], inp["k"], inp["v"], inp["bt"], inp["ctx"], 0.125, kv, threads=4)
+    np.testing.assert_allclose(got, want, atol=1e-5, rtol=1e-5)
+    assert not got[1].any()
