@@ -14,12 +14,14 @@ kernel's duration is measured with HIP events recorded on the launch stream
 around each partition launch inside the same timed loop.
 
 Also measured (the "also" list): config 3 (GQA bf16 ragged decode), config 5
-(77 GB pool, 64-bit offsets), configs 4a/4b (MFMA causal prefill, TFLOP/s).
+(77 GB pool, 64-bit offsets), configs 4a/4b (MFMA causal prefill, TFLOP/s),
+and the KV-cache write of the 4a/4b prompts into their pools (GB/s).
 
 cpu_baseline: the reference's own scalar cpu_reference
 (rocm/hip/paged_attn_v1_hip.cpp:104-141, built into oracle/_ref), one thread,
 on a bounded sample of config 2's sequences, timed on this host; the GPU
-result for the sample is checked against it.
+result for the sample is checked against it.  cpu_extra: our SIMD/OpenMP
+port of it and torch's CPU SDPA on the gathered layout, 16 threads.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload decode_c2]
 """
@@ -143,15 +145,13 @@ class PrefillWorkload:
         self.q = torch.randn((B, S, H, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
         k_new = torch.randn((B, S, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
         v_new = torch.randn((B, S, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
-        # Write the prompt's K/V into the paged pool through the block table (untimed setup).
+        # Write the prompt's K/V into the paged pool with pa_write_kv (untimed setup).
         self.k = torch.zeros((nb, BS, HKV, D), device=dev, dtype=dtype)
         self.v = torch.zeros_like(self.k)
         tok = torch.arange(S, device=dev)
         bt = torch.from_numpy(perm).to(dev)
-        for b in range(B):
-            blk = bt[b, tok // BS]
-            self.k[blk, tok % BS] = k_new[b]
-            self.v[blk, tok % BS] = v_new[b]
+        slots = (bt[:, tok // BS].long() * BS + tok % BS).reshape(-1)
+        pa.write_kv(self.k, self.v, k_new.reshape(B * S, HKV, D), v_new.reshape(B * S, HKV, D), slots)
         self.bt = bt
         self.ctx = torch.full((B,), S, dtype=torch.int32, device=dev)
         self.out = torch.empty((B, S, H, D), device=dev, dtype=dtype)
@@ -170,6 +170,59 @@ class PrefillWorkload:
 
 
 # ------------------------------------------------------------------ timing --
+
+class WriteWorkload:
+    """KV-cache write: a prompt's K/V ([B*S, HKV, D]) into its paged pool at the
+    block table's slots (pa_write_kv), rotated over `copies` disjoint
+    (source, pool) pairs so each step reads and writes HBM, not cache."""
+
+    def __init__(self, pa, *, B, S, HKV, D, BS, dtype, seed, name, copies=8):
+        self.pa, self.name, self.dtype = pa, name, dtype
+        dev = torch.device("cuda:0")
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        rng = np.random.default_rng(seed)
+        pages = -(-S // BS)
+        nb, T = B * pages, B * S
+        tok = np.arange(S)
+        V = pa.view
+        self._keep, self.args = [], []
+        for _ in range(copies):
+            perm = rng.permutation(nb).reshape(B, pages)
+            slots = torch.from_numpy((perm[:, tok // BS] * BS + tok % BS).reshape(-1)).to(dev)
+            key = torch.randn((T, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+            val = torch.randn((T, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+            kc = torch.zeros((nb, BS, HKV, D), device=dev, dtype=dtype)
+            vc = torch.zeros_like(kc)
+            views = [V(kc), V(vc), V(key), V(val), V(slots)]
+            self._keep.append((slots, key, val, kc, vc, views))
+            self.args.append([C.byref(x) for x in views])
+        es = torch.tensor([], dtype=dtype).element_size()
+        self.bytes = 2.0 * T * HKV * D * 2 * es + T * 8  # K and V read + written, slot mapping
+        self.L = pa.lib()
+
+    def launch(self, i, stream, ev_mid=None):
+        rc = self.L.pa_write_kv(*self.args[i % len(self.args)], stream)
+        if rc != 0:
+            raise RuntimeError(self.pa.last_error())
+
+
+# The prompt K/V of configs 4a and 4b written into their paged pools.
+WRITE_CFG = {
+    "write_kv_c4a": dict(B=8, S=1024, HKV=12, D=64, dtype=torch.float16, seed=14),
+    "write_kv_c4b": dict(B=2, S=4096, HKV=32, D=128, dtype=torch.bfloat16, seed=16),
+}
+
+
+def write_record(work, steps, warmup):
+    ms, kms = timed(work, steps, warmup)
+    gbs = work.bytes / (kms * 1e-3) / 1e9
+    return {
+        "workload": work.name, "value": round(gbs, 1), "unit": "GB/s",
+        "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4), "ms_per_step": round(ms, 5),
+        "kernel_ms": round(kms, 5), "bytes_per_step": work.bytes, "dtype": str(work.dtype).replace("torch.", ""),
+    }
+
 
 def timed(work, steps, warmup):
     """(ms per step, mean dominant-kernel ms).
@@ -403,7 +456,7 @@ def main():
     ap.add_argument("--pools", type=int, default=6, help="rotated KV pools (config 2)")
     ap.add_argument("--workload", default="decode_c2",
                     choices=["decode_c2", "decode_c3", "decode_c5", "prefill_c4a", "prefill_c4b",
-                             "copy_calib"],
+                             "write_kv_c4a", "write_kv_c4b", "copy_calib"],
                     help="with --only: run just this workload's kernel loop (for profiling)")
     ap.add_argument("--only", action="store_true", help="time only --workload, print its record")
     ap.add_argument("--no-also", action="store_true", help="skip the secondary configs")
@@ -438,6 +491,9 @@ def main():
                     PrefillWorkload(pa, B=2, S=4096, H=32, HKV=32, D=128, BS=16, dtype=torch.bfloat16,
                                     seed=6, name="prefill_c4b"))
             print(json.dumps(prefill_record(work, args.steps, args.warmup)), flush=True)
+        elif w.startswith("write_kv"):
+            work = WriteWorkload(pa, BS=16, name=w, **WRITE_CFG[w])
+            print(json.dumps(write_record(work, args.steps, args.warmup)), flush=True)
         else:
             work = {"decode_c2": lambda: make_c2(pa, args.pools), "decode_c3": lambda: make_c3(pa, 2),
                     "decode_c5": lambda: make_c5(pa)}[w]()
@@ -491,6 +547,12 @@ def main():
             log(f"bench: {name}")
             w = PrefillWorkload(pa, BS=16, name=name, **kw)
             also.append(prefill_record(w, max(20, args.steps // 4), 5))
+            del w
+            torch.cuda.empty_cache()
+        for name, kw in WRITE_CFG.items():
+            log(f"bench: {name}")
+            w = WriteWorkload(pa, BS=16, name=name, **kw)
+            also.append(write_record(w, max(20, args.steps // 4), 5))
             del w
             torch.cuda.empty_cache()
     line["also"] = also

@@ -502,4 +502,76 @@ int paged_attention_prefill_wmma(pa_tensor_t* out, const pa_tensor_t* q,
                     "prefill kernel launch");
 }
 
+int pa_write_kv(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tensor_t* key,
+                const pa_tensor_t* value, const pa_tensor_t* slot_mapping, void* stream) {
+  int rc;
+  if ((rc = check_tensor(k_cache, "k_cache", 4, "[NB, BS, HKV, D]"))) return rc;
+  if ((rc = check_tensor(v_cache, "v_cache", 4, "[NB, BS, HKV, D]"))) return rc;
+  if ((rc = check_tensor(key, "key", 3, "[T, HKV, D]"))) return rc;
+  if ((rc = check_tensor(value, "value", 3, "[T, HKV, D]"))) return rc;
+  if ((rc = check_tensor(slot_mapping, "slot_mapping", 1, "[T]"))) return rc;
+  const int cd = k_cache->dtype, sd = key->dtype;
+  if (cd != kF16 && cd != kBF16 && cd != kF32)
+    return fail(PA_ERR_INVALID_ARGUMENT, "k_cache must be float16, bfloat16 or float32 (got %s)", dtype_name(cd));
+  if (v_cache->dtype != cd) return fail(PA_ERR_INVALID_ARGUMENT, "v_cache must have the dtype of k_cache");
+  if (sd != kF16 && sd != kBF16 && sd != kF32)
+    return fail(PA_ERR_INVALID_ARGUMENT, "key must be float16, bfloat16 or float32 (got %s)", dtype_name(sd));
+  if (value->dtype != sd) return fail(PA_ERR_INVALID_ARGUMENT, "value must have the dtype of key");
+  if (slot_mapping->dtype != kI32 && slot_mapping->dtype != kI64)
+    return fail(PA_ERR_INVALID_ARGUMENT, "slot_mapping must be int32 or int64");
+  for (int i = 0; i < 4; ++i)
+    if (v_cache->shape[i] != k_cache->shape[i])
+      return fail(PA_ERR_INVALID_ARGUMENT, "v_cache must have the shape of k_cache");
+  const int64_t NB = k_cache->shape[0], BS = k_cache->shape[1], HKV = k_cache->shape[2], D = k_cache->shape[3];
+  const int64_t T = key->shape[0];
+  for (int i = 0; i < 3; ++i)
+    if (value->shape[i] != key->shape[i]) return fail(PA_ERR_INVALID_ARGUMENT, "value must have the shape of key");
+  if (key->shape[1] != HKV || key->shape[2] != D)
+    return fail(PA_ERR_INVALID_ARGUMENT, "key must be [T, %lld, %lld] to match k_cache", (long long)HKV,
+                (long long)D);
+  if (slot_mapping->shape[0] != T) return fail(PA_ERR_INVALID_ARGUMENT, "slot_mapping must have T entries");
+  if (T > 1 && slot_mapping->stride[0] != 1) return fail(PA_ERR_INVALID_ARGUMENT, "slot_mapping must be contiguous");
+  if (D <= 0 || D % 8 != 0) return fail(PA_ERR_UNSUPPORTED, "head_dim must be a positive multiple of 8");
+  if (BS <= 0) return fail(PA_ERR_INVALID_ARGUMENT, "block_size must be positive");
+  if (NB * BS >= (1LL << 31) || T * HKV * (D / 8) >= (1LL << 40))
+    return fail(PA_ERR_UNSUPPORTED, "problem too large for 32-bit slot indices");
+  const int ces = dtype_bytes(cd), ses = dtype_bytes(sd);
+  for (const pa_tensor_t* t : {(const pa_tensor_t*)k_cache, (const pa_tensor_t*)v_cache}) {
+    if (t->stride[3] != 1) return fail(PA_ERR_INVALID_ARGUMENT, "k_cache/v_cache must have a contiguous last dimension");
+    for (int i = 0; i < 3; ++i) {
+      if (t->stride[i] < 0) return fail(PA_ERR_UNSUPPORTED, "k_cache/v_cache strides must be non-negative");
+      if (((t->stride[i] * ces) & 15) != 0 && t->shape[i] > 1)
+        return fail(PA_ERR_UNSUPPORTED, "k_cache/v_cache strides must be multiples of 16 bytes");
+    }
+    if ((reinterpret_cast<uintptr_t>(t->data) & 15) != 0)
+      return fail(PA_ERR_UNSUPPORTED, "k_cache/v_cache must be 16-byte aligned");
+  }
+  for (const pa_tensor_t* t : {key, value}) {
+    if (t->stride[2] != 1) return fail(PA_ERR_INVALID_ARGUMENT, "key/value must have a contiguous last dimension");
+    for (int i = 0; i < 2; ++i) {
+      if (t->stride[i] < 0) return fail(PA_ERR_UNSUPPORTED, "key/value strides must be non-negative");
+      if (((t->stride[i] * ses) & 15) != 0 && t->shape[i] > 1)
+        return fail(PA_ERR_UNSUPPORTED, "key/value token and head strides must be multiples of 16 bytes");
+    }
+    if ((reinterpret_cast<uintptr_t>(t->data) & 15) != 0)
+      return fail(PA_ERR_UNSUPPORTED, "key/value must be 16-byte aligned");
+  }
+  if (T == 0 || NB == 0 || HKV == 0) return PA_OK;
+  WriteParams p;
+  memset(&p, 0, sizeof(p));
+  p.kc = k_cache->data; p.vc = v_cache->data;
+  p.key = key->data; p.value = value->data; p.slots = slot_mapping->data;
+  p.kc_sb = k_cache->stride[0]; p.kc_st = k_cache->stride[1]; p.kc_sh = k_cache->stride[2];
+  p.vc_sb = v_cache->stride[0]; p.vc_st = v_cache->stride[1]; p.vc_sh = v_cache->stride[2];
+  p.key_st = key->stride[0]; p.key_sh = key->stride[1];
+  p.val_st = value->stride[0]; p.val_sh = value->stride[1];
+  p.nslots = NB * BS;
+  p.T = (int32_t)std::min<int64_t>(T, INT32_MAX);
+  if (T > INT32_MAX) return fail(PA_ERR_UNSUPPORTED, "too many tokens for one call");
+  p.HKV = (int32_t)HKV; p.D = (int32_t)D; p.BS = (int32_t)BS;
+  p.src_dtype = sd; p.cache_dtype = cd; p.slot_i64 = slot_mapping->dtype == kI64;
+  p.bs_div = make_fastdiv((uint32_t)BS);
+  return hip_status(launch_write_kv(p, static_cast<hipStream_t>(stream)), "KV write kernel launch");
+}
+
 }  // extern "C"

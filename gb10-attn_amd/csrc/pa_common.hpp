@@ -97,10 +97,28 @@ struct PrefillParams {
   uint32_t q_xor;
 };
 
+// KV-cache write: new [T, HKV, D] rows -> paged pool slots (element strides).
+struct WriteParams {
+  void* kc;            // k_cache / v_cache [NB, BS, HKV, D]
+  void* vc;
+  const void* key;     // [T, HKV, D]
+  const void* value;
+  const void* slots;   // [T] int32 or int64
+  int64_t kc_sb, kc_st, kc_sh;
+  int64_t vc_sb, vc_st, vc_sh;
+  int64_t key_st, key_sh;
+  int64_t val_st, val_sh;
+  int64_t nslots;      // NB * BS (< 2^31)
+  int32_t T, HKV, D, BS;
+  int32_t src_dtype, cache_dtype, slot_i64;
+  FastDiv bs_div;
+};
+
 // Host launchers (defined in the kernel translation units).
 hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int gc, hipStream_t stream);
 hipError_t launch_reduce(const ReduceParams& p, hipStream_t stream);
 hipError_t launch_prefill_mfma(const PrefillParams& p, int kv_dtype, hipStream_t stream);
+hipError_t launch_write_kv(const WriteParams& p, hipStream_t stream);
 
 // Heads per decode work-group for a GQA group of G query heads.
 inline int decode_heads_per_wg(int G) {

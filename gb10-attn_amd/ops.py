@@ -166,3 +166,47 @@ def plan_partitions(num_seqs, num_heads, num_kv_heads, head_dim, max_context, nu
     check(lib().pa_plan_partitions(int(num_seqs), int(num_heads), int(num_kv_heads), int(head_dim),
                                    int(max_context), int(num_compute_units), C.byref(a), C.byref(b)))
     return int(a.value), int(b.value)
+
+
+def write_kv(k_cache, v_cache, key, value, slot_mapping):
+    """KV-cache write: key/value [T, HKV, D] (fp32/fp16/bf16, any token/head
+    strides) into k_cache/v_cache [NB, BS, HKV, D] at slot_mapping[t]
+    (block slot // BS, row slot % BS; negative slots skipped), converted to the
+    cache dtype with round-to-nearest-even.  In place; returns nothing."""
+    for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache"), (key, "key"), (value, "value")):
+        if not t.is_cuda:
+            raise RuntimeError(f"{n} must be on CUDA")
+    if key.dim() != 3 or value.dim() != 3:
+        raise RuntimeError("key/value must be [T, HKV, D]")
+    if not _kv_ok(k_cache) or not _kv_ok(v_cache):
+        raise RuntimeError("k_cache/v_cache must be 16-byte aligned [NB, BS, HKV, D] views with a contiguous last dim")
+    if key.stride(2) != 1 or key.data_ptr() % 16:
+        key = key.contiguous()
+    if value.stride(2) != 1 or value.data_ptr() % 16:
+        value = value.contiguous()
+    if slot_mapping.dtype not in (torch.int32, torch.int64):
+        slot_mapping = slot_mapping.to(torch.int64)
+    slot_mapping = slot_mapping.to(key.device).contiguous()
+    with torch.cuda.device(key.device):
+        check(lib().pa_write_kv(C.byref(view(k_cache)), C.byref(view(v_cache)), C.byref(view(key)),
+                                C.byref(view(value)), C.byref(view(slot_mapping)), _stream(key.device)))
+
+
+def write_kv_blocks(kv_pool, block_ids, start, k, v):
+    """The serving engine's write_kv(block_ids, start, k, v): one sequence's
+    K/V for all layers, k/v [n_layer, n_head, ctx, head_dim] (host numpy or
+    torch), into kv_pool [n_layer, 2, NB, BS, HKV, D] at token positions
+    start .. start + ctx - 1 of the sequence whose pages are block_ids.  Each
+    layer is one pa_write_kv call on the [ctx, HKV, D] view of k[layer]."""
+    L, _, NB, BS, HKV, D = kv_pool.shape
+    k = torch.as_tensor(k).to(kv_pool.device)
+    v = torch.as_tensor(v).to(kv_pool.device)
+    ctx = k.shape[2]
+    pos = torch.arange(start, start + ctx, device=kv_pool.device)
+    blocks = torch.as_tensor(block_ids, dtype=torch.int64, device=kv_pool.device)
+    if (start + ctx + BS - 1) // BS > blocks.numel():
+        raise RuntimeError("block_ids do not cover the written positions")
+    slots = blocks[pos // BS] * BS + pos % BS
+    for layer in range(L):
+        write_kv(kv_pool[layer, 0], kv_pool[layer, 1], k[layer].permute(1, 0, 2), v[layer].permute(1, 0, 2), slots)
+

@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 1
+#define PA_ABI_VERSION 2
 #define PA_MAX_DIMS 4
 
 typedef enum pa_dtype {
@@ -164,12 +164,28 @@ int paged_attention_prefill(pa_tensor_t* out, const pa_tensor_t* q, const pa_ten
 /* Causal (chunked) prefill on CDNA4 matrix cores.  Replaces
  * paged_attention_prefill_wmma(), kernels/paged_attn_wmma.h:13-15
  * (kernels/paged_attn_wmma.cu:212-274).  K/V fp16 (as the reference) or
- * bf16; Q and the probabilities are rounded to the KV type before each
- * matrix product, accumulation is fp32.  D in {32, 64, 128}. */
+ * bf16; Q is rounded to the KV type (split hi + lo when it arrives in
+ * another type), the probabilities to fp16 (bf16 hi + lo when a bf16 V value
+ * does not fit fp16), accumulation is fp32.  D in {32, 64, 128, 256}. */
 int paged_attention_prefill_wmma(pa_tensor_t* out, const pa_tensor_t* q,
                                  const pa_tensor_t* k_cache, const pa_tensor_t* v_cache,
                                  const pa_tensor_t* block_tables,
                                  const pa_tensor_t* context_lens, double scale, void* stream);
+
+/* KV-cache write ("reshape and cache"): token t's K and V rows, key[t] and
+ * value[t] ([T, HKV, D], any non-negative token/head strides, 16-byte aligned
+ * rows), go to block slot_mapping[t] / BS, row slot_mapping[t] % BS of
+ * k_cache / v_cache ([NB, BS, HKV, D] views, as the attention entry points
+ * take them), converted to the cache's type with round-to-nearest-even.
+ * A negative slot (padding) or one >= NB * BS is skipped.  slot_mapping is
+ * int32 or int64; key/value and the caches are float32, float16 or bfloat16.
+ * Replaces the reference engine's TorchBlockAllocator.write_kv (external to
+ * the reference; its call sites are harness/repro_crash.py:52-58 and
+ * results/c001-20260901-223111/bench_b64_c2048.txt:16-22): one sequence's
+ * [n_head, ctx, head_dim] layer slice is a strided [T, HKV, D] key with
+ * slot_mapping[t] = block_ids[t / BS] * BS + t % BS. */
+int pa_write_kv(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tensor_t* key,
+                const pa_tensor_t* value, const pa_tensor_t* slot_mapping, void* stream);
 
 #ifdef __cplusplus
 }

@@ -269,6 +269,26 @@ def prefill(q, k, v, bt, ctx, scale, kv_dtype="f32") -> np.ndarray:
     return out
 
 
+def write_kv(k_cache, v_cache, key, value, slots, cache_dtype, src_dtype):
+    """KV-cache write, in place on host caches [NB, BS, HKV, D] (storage per NP_OF):
+    token t's rows key[t], value[t] ([T, HKV, D], stored as src_dtype) go to
+    block slots[t] // BS, row slots[t] % BS, rounded to the cache type (round
+    to nearest even; the same 16-bit type is copied bit for bit).  A negative
+    slot or one >= NB * BS is skipped.  This restates the serving engine's
+    write_kv layout (token j of a sequence -> block_ids[j // BS], row j % BS;
+    external to the reference, called at harness/repro_crash.py:52-58)."""
+    NB, BS = k_cache.shape[:2]
+    for t, s in enumerate(np.asarray(slots).tolist()):
+        if s < 0 or s >= NB * BS:
+            continue
+        b, o = divmod(int(s), BS)
+        for cache, src in ((k_cache, key), (v_cache, value)):
+            if src_dtype == cache_dtype:
+                cache[b, o] = src[t]
+            else:
+                cache[b, o] = quantize(to_float(src[t], src_dtype), cache_dtype)
+
+
 def gather(k, v, bt_row, n, kvh, kv_dtype="f32"):
     """K and V rows of tokens [0, n) of one sequence and KV head -> ([n,D], [n,D]) float32."""
     kv = _kv(k, v, kv_dtype)

@@ -27,7 +27,7 @@ def header_functions():
 
 def test_library_loads_and_exports_header(pa):
     L = pa.lib()
-    assert L.pa_abi_version() == 1
+    assert L.pa_abi_version() == 2
     declared = header_functions()
     assert declared == sorted(pa.EXPORTS)
     syms = subprocess.run(["nm", "-D", "--defined-only", str(pa.LIB_PATH)], capture_output=True,
@@ -211,3 +211,57 @@ def test_import_without_library_fails_loudly(tmp_path):
         sys.modules.pop("pkgcopy", None)
         for k in [k for k in sys.modules if k.startswith("pkgcopy.")]:
             sys.modules.pop(k)
+
+
+def write_args(pa, T_=5, HKV=2, D=64, NB=10, BS=16, cdt=F16, sdt=F32, slot=I64):
+    return dict(kc=T(pa, [NB, BS, HKV, D], cdt), vc=T(pa, [NB, BS, HKV, D], cdt), key=T(pa, [T_, HKV, D], sdt),
+                val=T(pa, [T_, HKV, D], sdt), slots=T(pa, [T_], slot))
+
+
+def write_call(pa, a):
+    L = pa.lib()
+    rc = L.pa_write_kv(C.byref(a["kc"]), C.byref(a["vc"]), C.byref(a["key"]), C.byref(a["val"]),
+                       C.byref(a["slots"]), None)
+    return rc, L.pa_last_error().decode()
+
+
+@pytest.mark.parametrize("case,code,msg", [
+    (dict(cdt=F64), 1, "k_cache must be float16, bfloat16 or float32"),
+    (dict(sdt=I32), 1, "key must be float16, bfloat16 or float32"),
+    (dict(slot=F32), 1, "slot_mapping must be int32 or int64"),
+    (dict(D=60), 2, "head_dim must be a positive multiple of 8"),
+])
+def test_write_kv_rejections(pa, case, code, msg):
+    rc, err = write_call(pa, write_args(pa, **case))
+    assert rc == code and msg in err, (rc, err)
+
+
+def test_write_kv_shape_rejections(pa):
+    a = write_args(pa)
+    a["key"] = T(pa, [5, 3, 64], F32)
+    a["val"] = T(pa, [5, 3, 64], F32)
+    rc, err = write_call(pa, a)
+    assert rc == 1 and "key must be [T, 2, 64]" in err
+    a = write_args(pa)
+    a["slots"] = T(pa, [4], I64)
+    rc, err = write_call(pa, a)
+    assert rc == 1 and "slot_mapping must have T entries" in err
+    a = write_args(pa)
+    a["val"] = T(pa, [5, 2, 64], F16)
+    rc, err = write_call(pa, a)
+    assert rc == 1 and "value must have the dtype of key" in err
+    a = write_args(pa)
+    a["key"] = T(pa, [5, 2, 64], F32, data=FAKE + 4)
+    rc, err = write_call(pa, a)
+    assert rc == 2 and "key/value must be 16-byte aligned" in err
+    a = write_args(pa)
+    a["key"] = T(pa, [5, 2, 64], F16, stride=[130, 65, 1])
+    a["val"] = T(pa, [5, 2, 64], F16)
+    a["key"].dtype = F16
+    rc, err = write_call(pa, write_args(pa, sdt=F16) | {"key": a["key"]})
+    assert rc == 2 and "multiples of 16 bytes" in err
+
+
+def test_write_kv_zero_tokens_is_a_no_op(pa):
+    rc, err = write_call(pa, write_args(pa, T_=0))
+    assert rc == 0, err

@@ -380,3 +380,40 @@ def test_simd_baseline_matches_scalar_oracle(kv):
     got = oracle.decode_simd(inp["q_f32"], inp["k"], inp["v"], inp["bt"], inp["ctx"], 0.125, kv, threads=4)
     np.testing.assert_allclose(got, want, atol=1e-5, rtol=1e-5)
     assert not got[1].any()
+
+
+def test_write_kv_oracle_pins():
+    """The write restatement against library routines: f32 -> f16 is numpy's
+    float16 cast, f32 -> bf16 is torch's bfloat16 cast (both round to nearest
+    even), same-type writes copy bits; written rows read back through the
+    block-table gather at the engine's slot layout; padding slots write nothing."""
+    rng = np.random.default_rng(5)
+    NB, BS, HKV, D, T = 6, 4, 2, 16, 9
+    key = (rng.standard_normal((T, HKV, D)) * 3).astype(np.float32)
+    val = (rng.standard_normal((T, HKV, D)) * 3).astype(np.float32)
+    blocks = np.array([4, 1, 5], np.int64)
+    slots = blocks[np.arange(T) // BS] * BS + np.arange(T) % BS
+    slots[3] = -1
+    for cd in ("f16", "bf16"):
+        kc = np.zeros((NB, BS, HKV, D), oracle.NP_OF[cd])
+        vc = np.zeros_like(kc)
+        oracle.write_kv(kc, vc, key, val, slots, cd, "f32")
+        if cd == "f16":
+            want_k = key.astype(np.float16)
+        else:
+            want_k = torch.from_numpy(key).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        for t, s in enumerate(slots):
+            if s < 0:
+                assert not kc[blocks[t // BS], t % BS].any()
+                continue
+            assert np.array_equal(kc[s // BS, s % BS], want_k[t])
+        bt = np.zeros((1, 3), np.int32)
+        bt[0] = blocks
+        gk, gv = oracle.gather(kc, vc, bt[0], T, 1, cd)
+        live = slots >= 0
+        np.testing.assert_array_equal(gk[live], oracle.to_float(want_k[:, 1], cd)[live])
+    kc = np.zeros((NB, BS, HKV, D), np.uint16)
+    vc = np.zeros_like(kc)
+    bits = rng.integers(0, 1 << 16, (T, HKV, D)).astype(np.uint16)
+    oracle.write_kv(kc, vc, bits, bits, slots, "bf16", "bf16")
+    assert np.array_equal(kc[slots[0] // BS, slots[0] % BS], bits[0])
