@@ -224,6 +224,53 @@ def write_record(work, steps, warmup):
     }
 
 
+def call_overhead(pa, calls=3000):
+    """Wall time per call of a tiny v3 decode (B=1, H=12, ctx=64: microseconds of
+    GPU work) through each binding, so host cost dominates: the C-ABI with
+    prebuilt descriptors (ctypes), the Python mirror (ops.paged_attention_v3),
+    the torch operator (torch.ops.gb10_attn), and a HIP graph replay of it."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+    q = torch.randn((1, 12, 64), generator=g, device=dev).half()
+    k = torch.randn((4, 16, 12, 64), generator=g, device=dev).half()
+    v = torch.randn((4, 16, 12, 64), generator=g, device=dev).half()
+    bt = torch.arange(4, dtype=torch.int32, device=dev)[None]
+    ctx = torch.full((1,), 64, dtype=torch.int32, device=dev)
+    out = torch.empty((1, 12, 64), device=dev)
+    V = pa.view
+    views = [V(out), V(q), V(k), V(v), V(bt), V(ctx)]
+    args = [C.byref(x) for x in views]
+    L = pa.lib()
+    sp = torch.cuda.current_stream().cuda_stream
+    ops = pa.torch_ops()
+
+    def per_call(fn):
+        for _ in range(50):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        torch.cuda.synchronize()
+        return round((time.perf_counter() - t0) / calls * 1e6, 2)
+
+    res = {"c_abi_ctypes_us": per_call(lambda: L.paged_attention_v3(*args, 0.125, 0, None, 0, sp)),
+           "python_mirror_us": per_call(lambda: pa.paged_attention_v3(q, k, v, bt, ctx, 0.125, 0)),
+           "torch_op_us": per_call(lambda: ops.paged_attention_v3(q, k, v, bt, ctx, 0.125, 0))}
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.paged_attention_v3(q, k, v, bt, ctx, 0.125, 0)
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(graph):
+        ops.paged_attention_v3(q, k, v, bt, ctx, 0.125, 0)
+    res["graph_replay_us"] = per_call(graph.replay)
+    return {"workload": "call_overhead", "unit": "us per call", "case": "v3 decode B=1 H=12 D=64 ctx=64 fp16",
+            **res}
+
+
 def timed(work, steps, warmup):
     """(ms per step, mean dominant-kernel ms).
 
@@ -456,7 +503,7 @@ def main():
     ap.add_argument("--pools", type=int, default=6, help="rotated KV pools (config 2)")
     ap.add_argument("--workload", default="decode_c2",
                     choices=["decode_c2", "decode_c3", "decode_c5", "prefill_c4a", "prefill_c4b",
-                             "write_kv_c4a", "write_kv_c4b", "copy_calib"],
+                             "write_kv_c4a", "write_kv_c4b", "call_overhead", "copy_calib"],
                     help="with --only: run just this workload's kernel loop (for profiling)")
     ap.add_argument("--only", action="store_true", help="time only --workload, print its record")
     ap.add_argument("--no-also", action="store_true", help="skip the secondary configs")
@@ -491,6 +538,8 @@ def main():
                     PrefillWorkload(pa, B=2, S=4096, H=32, HKV=32, D=128, BS=16, dtype=torch.bfloat16,
                                     seed=6, name="prefill_c4b"))
             print(json.dumps(prefill_record(work, args.steps, args.warmup)), flush=True)
+        elif w == "call_overhead":
+            print(json.dumps(call_overhead(pa)), flush=True)
         elif w.startswith("write_kv"):
             work = WriteWorkload(pa, BS=16, name=w, **WRITE_CFG[w])
             print(json.dumps(write_record(work, args.steps, args.warmup)), flush=True)
@@ -555,6 +604,8 @@ def main():
             also.append(write_record(w, max(20, args.steps // 4), 5))
             del w
             torch.cuda.empty_cache()
+        log("bench: per-call host overhead")
+        also.append(call_overhead(pa))
     line["also"] = also
     print(json.dumps(line), flush=True)
 

@@ -16,6 +16,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libpagedattn.so"
+TORCH_LIB = PKG / "libpagedattn_torch.so"
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.environ.get("HIPCC", f"{ROCM}/bin/hipcc")
 ARCH = "gfx950"
@@ -55,6 +56,30 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+def build_torch_ops(verbose: bool = False) -> Path:
+    """libpagedattn_torch.so: the torch.ops.gb10_attn operators (csrc/torch_ext.cpp),
+    host C++ against torch's ROCm headers, linked to libpagedattn.so by $ORIGIN."""
+    import torch
+    import torch.utils.cpp_extension as cx
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    inc = [f"-I{d}" for d in cx.include_paths()] + [f"-I{ROCM}/include"]
+    libdirs = cx.library_paths()
+    tmp = TORCH_LIB.with_suffix(".so.tmp")
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", *inc, str(CSRC / "torch_ext.cpp"), "-o", str(tmp),
+           *[f"-L{d}" for d in libdirs], *[f"-Wl,-rpath,{d}" for d in libdirs],
+           f"-L{PKG}", "-lpagedattn", "-Wl,-rpath,$ORIGIN",
+           "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"torch extension build failed:\n{r.stderr[-6000:]}")
+    os.replace(tmp, TORCH_LIB)
+    if verbose:
+        print(f"built {TORCH_LIB}")
+    return TORCH_LIB
+
+
 if __name__ == "__main__":
     build(verbose=True)
+    build_torch_ops(verbose=True)
     sys.exit(0)

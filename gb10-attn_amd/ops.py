@@ -210,3 +210,17 @@ def write_kv_blocks(kv_pool, block_ids, start, k, v):
     for layer in range(L):
         write_kv(kv_pool[layer, 0], kv_pool[layer, 1], k[layer].permute(1, 0, 2), v[layer].permute(1, 0, 2), slots)
 
+
+def torch_ops():
+    """The same launchers as PyTorch operators, torch.ops.gb10_attn.* (built from
+    csrc/torch_ext.cpp into libpagedattn_torch.so): the reference's exact
+    torch::Tensor signatures for callers that bind them from C++ or TorchScript,
+    with no Python/ctypes work per call.  Raises ImportError when not built."""
+    from ._lib import LIB_PATH
+    path = LIB_PATH.with_name("libpagedattn_torch.so")
+    if not path.exists():
+        raise ImportError(f"{path} is missing: build it with __graft_entry__.build()")
+    if not hasattr(torch.ops, "gb10_attn") or not hasattr(torch.ops.gb10_attn, "paged_attention_v3"):
+        torch.ops.load_library(str(path))
+    return torch.ops.gb10_attn
+

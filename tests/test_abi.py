@@ -265,3 +265,21 @@ def test_write_kv_shape_rejections(pa):
 def test_write_kv_zero_tokens_is_a_no_op(pa):
     rc, err = write_call(pa, write_args(pa, T_=0))
     assert rc == 0, err
+
+
+def test_torch_ops_load_with_reference_signatures(pa):
+    """torch.ops.gb10_attn carries the reference's kernels/*.h signatures (loads without a GPU)."""
+    ops = pa.torch_ops()
+    want = {
+        "paged_attention": "(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, Tensor context_lens, float scale) -> Tensor",
+        "paged_attention_v3": "(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, Tensor context_lens, float scale, int num_splits) -> Tensor",
+        "choose_num_splits": "(int num_seqs, int num_heads, int max_context) -> int",
+        "paged_attention_prefill_wmma": "(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, Tensor context_lens, float scale) -> Tensor",
+    }
+    for name, sig in want.items():
+        schema = str(getattr(ops, name).default._schema)
+        assert schema == f"gb10_attn::{name}{sig}", schema
+    import torch
+    with pytest.raises(RuntimeError, match="q must be on CUDA"):
+        ops.paged_attention(torch.zeros(1, 4, 64), torch.zeros(1, 16, 4, 64), torch.zeros(1, 16, 4, 64),
+                            torch.zeros(1, 1, dtype=torch.int32), torch.ones(1, dtype=torch.int32), 0.1)
