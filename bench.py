@@ -224,6 +224,66 @@ def write_record(work, steps, warmup):
     }
 
 
+class MixedWorkload:
+    """Mixed decode + prefill batch (GPT-2 geometry, fp16): `nd` sequences decoding
+    one token at context 2048 and `npf` sequences prefilling a `chunk`-token
+    chunk at context 2048, in one pool.  launch(): one varlen MFMA call;
+    launch_split(): a v3 decode of the decoders plus a uniform MFMA prefill of
+    the chunks (two launches)."""
+
+    def __init__(self, pa, nd=64, npf=4, chunk=256, ctx=2048, H=12, D=64, BS=16, seed=21):
+        self.pa, self.name = pa, "mixed_c2"
+        dev = torch.device("cuda:0")
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        rng = np.random.default_rng(seed)
+        B, pages = nd + npf, ctx // BS
+        self.k = torch.randn((B * pages, BS, H, D), generator=g, device=dev).half()
+        self.v = torch.randn((B * pages, BS, H, D), generator=g, device=dev).half()
+        self.bt = torch.from_numpy(rng.permutation(B * pages).astype(np.int32).reshape(B, pages)).to(dev)
+        self.ctx = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+        qlens = [1] * nd + [chunk] * npf
+        self.q = torch.randn((sum(qlens), H, D), generator=g, device=dev).half()
+        self.cu = torch.tensor(np.concatenate([[0], np.cumsum(qlens)]), dtype=torch.int32, device=dev)
+        self.max_q = chunk
+        self.scale = 1.0 / float(np.sqrt(D))
+        self.q_dec = self.q[:nd].contiguous()
+        self.q_pf = self.q[nd:].reshape(npf, chunk, H, D).contiguous()
+        self.out = torch.empty_like(self.q)
+        self.out_dec = torch.empty_like(self.q_dec)
+        self.out_pf = torch.empty_like(self.q_pf)
+        self.nd, self.npf, self.chunk = nd, npf, chunk
+        self.tokens = sum(qlens)
+        self.kv_bytes = 2.0 * B * ctx * H * D * 2
+        self.flops = 4.0 * D * H * (nd * ctx + npf * sum(ctx - chunk + r + 1 for r in range(chunk)))
+
+    def launch(self, i, stream, ev_mid=None):
+        self.pa.paged_attention_prefill_varlen(self.q, self.k, self.v, self.bt, self.ctx, self.cu, self.max_q,
+                                               self.scale, out=self.out)
+
+    def launch_split(self, i, stream, ev_mid=None):
+        nd = self.nd
+        self.pa.paged_attention_v3(self.q_dec, self.k, self.v, self.bt[:nd], self.ctx[:nd], self.scale, 0,
+                                   out=self.out_dec)
+        self.pa.paged_attention_prefill_wmma(self.q_pf, self.k, self.v, self.bt[nd:], self.ctx[nd:], self.scale,
+                                             out=self.out_pf)
+
+
+def mixed_record(pa, steps, warmup):
+    w = MixedWorkload(pa)
+    ms, _ = timed(w, steps, warmup)
+
+    class Split:
+        launch = w.launch_split
+    ms_split, _ = timed(Split(), steps, warmup)
+    return {"workload": w.name, "unit": "ms per step",
+            "case": f"{w.nd} decode rows + {w.npf} x {w.chunk}-token prefill chunks, ctx 2048, H=12 D=64 fp16",
+            "varlen_ms": round(ms, 5), "split_ms": round(ms_split, 5),
+            "varlen_tokens_per_s": round(w.tokens / (ms * 1e-3), 1),
+            "varlen_kv_GBs": round(w.kv_bytes / (ms * 1e-3) / 1e9, 1),
+            "flops_per_step": w.flops}
+
+
 def call_overhead(pa, calls=3000):
     """Wall time per call of a tiny v3 decode (B=1, H=12, ctx=64: microseconds of
     GPU work) through each binding, so host cost dominates: the C-ABI with
@@ -503,7 +563,7 @@ def main():
     ap.add_argument("--pools", type=int, default=6, help="rotated KV pools (config 2)")
     ap.add_argument("--workload", default="decode_c2",
                     choices=["decode_c2", "decode_c3", "decode_c5", "prefill_c4a", "prefill_c4b",
-                             "write_kv_c4a", "write_kv_c4b", "call_overhead", "copy_calib"],
+                             "write_kv_c4a", "write_kv_c4b", "call_overhead", "mixed_c2", "copy_calib"],
                     help="with --only: run just this workload's kernel loop (for profiling)")
     ap.add_argument("--only", action="store_true", help="time only --workload, print its record")
     ap.add_argument("--no-also", action="store_true", help="skip the secondary configs")
@@ -538,6 +598,8 @@ def main():
                     PrefillWorkload(pa, B=2, S=4096, H=32, HKV=32, D=128, BS=16, dtype=torch.bfloat16,
                                     seed=6, name="prefill_c4b"))
             print(json.dumps(prefill_record(work, args.steps, args.warmup)), flush=True)
+        elif w == "mixed_c2":
+            print(json.dumps(mixed_record(pa, args.steps, args.warmup)), flush=True)
         elif w == "call_overhead":
             print(json.dumps(call_overhead(pa)), flush=True)
         elif w.startswith("write_kv"):
@@ -604,6 +666,9 @@ def main():
             also.append(write_record(w, max(20, args.steps // 4), 5))
             del w
             torch.cuda.empty_cache()
+        log("bench: mixed decode + prefill batch")
+        also.append(mixed_record(pa, max(20, args.steps // 4), 5))
+        torch.cuda.empty_cache()
         log("bench: per-call host overhead")
         also.append(call_overhead(pa))
     line["also"] = also

@@ -24,7 +24,8 @@ EXPORTS = (
     "pa_abi_version", "pa_last_error", "paged_attention", "paged_attention_v2",
     "paged_attention_v3", "paged_attention_v3_workspace_size", "pa_v3_partition", "pa_v3_reduce",
     "choose_num_splits", "choose_num_splits_for", "pa_plan_partitions",
-    "paged_attention_prefill", "paged_attention_prefill_wmma", "pa_write_kv",
+    "paged_attention_prefill", "paged_attention_prefill_wmma", "paged_attention_prefill_varlen",
+    "pa_write_kv",
 )
 
 
@@ -88,6 +89,8 @@ def lib() -> C.CDLL:
     L.choose_num_splits_for.argtypes = [i64, i64, i64, i64]
     L.pa_plan_partitions.restype = C.c_int
     L.pa_plan_partitions.argtypes = [i64, i64, i64, i64, i64, i64, C.POINTER(i64), C.POINTER(i64)]
+    L.paged_attention_prefill_varlen.restype = C.c_int
+    L.paged_attention_prefill_varlen.argtypes = six + [T, i64, C.c_double, P]
     L.pa_write_kv.restype = C.c_int
     L.pa_write_kv.argtypes = [T, T, T, T, T, P]
     _lib = L

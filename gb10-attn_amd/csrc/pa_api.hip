@@ -342,6 +342,51 @@ int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const p
   return PA_OK;
 }
 
+// MFMA prefill launch for checked arguments; cu != null selects the
+// variable-length layout (rows cu[b] .. cu[b+1] of a packed [T, H, D] q/out).
+int run_prefill_mfma(DecodeArgs& a, const pa_tensor_t* q, const int32_t* cu, int64_t T, double scale,
+                     void* stream) {
+  // kernels/paged_attn_wmma.cu:220-223 requires fp16; bf16 is served as well.
+  if (a.kv_dtype != kF16 && a.kv_dtype != kBF16)
+    return fail(PA_ERR_INVALID_ARGUMENT, "the MFMA path needs an fp16 or bf16 KV cache");
+  if (a.p.D > 256) return fail(PA_ERR_UNSUPPORTED, "unsupported head_dim for the MFMA path: %d", a.p.D);
+  if ((int64_t)a.p.B * a.p.Sq * a.p.H == 0) return PA_OK;
+  if ((reinterpret_cast<uintptr_t>(q->data) & 15) != 0)
+    return fail(PA_ERR_UNSUPPORTED, "the MFMA path needs a 16-byte aligned q");
+  PrefillParams pp;
+  memset(&pp, 0, sizeof(pp));
+  const DecodeParams& p = a.p;
+  pp.q = p.q; pp.out = p.out; pp.k = p.k; pp.v = p.v;
+  pp.block_tables = p.block_tables; pp.context_lens = p.context_lens;
+  pp.k_sb = p.k_sb; pp.k_st = p.k_st; pp.k_sh = p.k_sh;
+  pp.v_sb = p.v_sb; pp.v_st = p.v_st; pp.v_sh = p.v_sh;
+  pp.bt_stride = p.bt_stride; pp.num_blocks = p.num_blocks;
+  pp.B = p.B; pp.S = p.Sq; pp.H = p.H; pp.HKV = p.HKV; pp.G = p.G; pp.D = p.D; pp.BS = p.BS; pp.MB = p.MB;
+  pp.q_dtype = p.q_dtype; pp.out_dtype = p.out_dtype;
+  pp.q_split = p.q_dtype != a.kv_dtype;
+  pp.bs_div = p.bs_div;
+  pp.cu_q = cu;
+  pp.q_total = T;
+  // The kernel applies the sign of the scale to q (exactly) and keeps the
+  // softmax scale positive, so the running max of raw scores orders as the scaled ones.
+  const double log2e = 1.4426950408889634;
+  pp.q_and = 0xffffffffu;
+  pp.q_xor = 0u;
+  pp.q_sign = 1.0f;
+  pp.qscale = (float)(scale * log2e);
+  if (scale < 0) {
+    pp.q_xor = 0x80008000u;
+    pp.q_sign = -1.0f;
+    pp.qscale = (float)(-scale * log2e);
+  } else if (scale == 0) {
+    pp.q_and = 0u;
+    pp.q_sign = 0.0f;
+    pp.qscale = 1.0f;
+  }
+  return hip_status(launch_prefill_mfma(pp, a.kv_dtype, static_cast<hipStream_t>(stream)),
+                    "prefill kernel launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -463,43 +508,41 @@ int paged_attention_prefill_wmma(pa_tensor_t* out, const pa_tensor_t* q,
   DecodeArgs a;
   int rc = check_args(out, q, k_cache, v_cache, block_tables, context_lens, scale, true, &a);
   if (rc) return rc;
-  // kernels/paged_attn_wmma.cu:220-223 requires fp16; bf16 is served as well.
-  if (a.kv_dtype != kF16 && a.kv_dtype != kBF16)
-    return fail(PA_ERR_INVALID_ARGUMENT, "the MFMA path needs an fp16 or bf16 KV cache");
-  if (a.p.D > 256) return fail(PA_ERR_UNSUPPORTED, "unsupported head_dim for the MFMA path: %d", a.p.D);
-  if ((int64_t)a.p.B * a.p.Sq * a.p.H == 0) return PA_OK;
-  if ((reinterpret_cast<uintptr_t>(q->data) & 15) != 0)
-    return fail(PA_ERR_UNSUPPORTED, "the MFMA path needs a 16-byte aligned q");
-  PrefillParams pp;
-  memset(&pp, 0, sizeof(pp));
-  const DecodeParams& p = a.p;
-  pp.q = p.q; pp.out = p.out; pp.k = p.k; pp.v = p.v;
-  pp.block_tables = p.block_tables; pp.context_lens = p.context_lens;
-  pp.k_sb = p.k_sb; pp.k_st = p.k_st; pp.k_sh = p.k_sh;
-  pp.v_sb = p.v_sb; pp.v_st = p.v_st; pp.v_sh = p.v_sh;
-  pp.bt_stride = p.bt_stride; pp.num_blocks = p.num_blocks;
-  pp.B = p.B; pp.S = p.Sq; pp.H = p.H; pp.HKV = p.HKV; pp.G = p.G; pp.D = p.D; pp.BS = p.BS; pp.MB = p.MB;
-  pp.q_dtype = p.q_dtype; pp.out_dtype = p.out_dtype;
-  pp.q_split = p.q_dtype != a.kv_dtype;
-  pp.bs_div = p.bs_div;
-  // The kernel applies the sign of the scale to q (exactly) and keeps the
-  // softmax scale positive, so the running max of raw scores orders as the scaled ones.
-  const double log2e = 1.4426950408889634;
-  pp.q_and = 0xffffffffu;
-  pp.q_xor = 0u;
-  pp.q_sign = 1.0f;
-  pp.qscale = (float)(scale * log2e);
-  if (scale < 0) {
-    pp.q_xor = 0x80008000u;
-    pp.q_sign = -1.0f;
-    pp.qscale = (float)(-scale * log2e);
-  } else if (scale == 0) {
-    pp.q_and = 0u;
-    pp.q_sign = 0.0f;
-    pp.qscale = 1.0f;
-  }
-  return hip_status(launch_prefill_mfma(pp, a.kv_dtype, static_cast<hipStream_t>(stream)),
-                    "prefill kernel launch");
+  return run_prefill_mfma(a, q, nullptr, 0, scale, stream);
+}
+
+int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                                   const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                                   const pa_tensor_t* context_lens, const pa_tensor_t* cu_seqlens_q,
+                                   int64_t max_q_len, double scale, void* stream) {
+  int rc;
+  if ((rc = check_tensor(q, "q", 3, "[T, H, D]"))) return rc;
+  if ((rc = check_tensor(out, "out", 3, "[T, H, D]"))) return rc;
+  if ((rc = check_tensor(block_tables, "block_tables", 2, "[B, MB]"))) return rc;
+  if ((rc = check_tensor(cu_seqlens_q, "cu_seqlens_q", 1, "[B + 1]"))) return rc;
+  for (int i = 0; i < 3; ++i)
+    if (out->shape[i] != q->shape[i]) return fail(PA_ERR_INVALID_ARGUMENT, "out must have the shape of q");
+  if (!is_contiguous(q)) return fail(PA_ERR_INVALID_ARGUMENT, "q must be contiguous");
+  if (!is_contiguous(out)) return fail(PA_ERR_INVALID_ARGUMENT, "out must be contiguous");
+  const int64_t B = block_tables->shape[0], T = q->shape[0];
+  if (cu_seqlens_q->dtype != kI32) return fail(PA_ERR_INVALID_ARGUMENT, "cu_seqlens_q must be int32");
+  if (cu_seqlens_q->shape[0] != B + 1) return fail(PA_ERR_INVALID_ARGUMENT, "cu_seqlens_q must have B + 1 entries");
+  if (cu_seqlens_q->stride[0] != 1) return fail(PA_ERR_INVALID_ARGUMENT, "cu_seqlens_q must be contiguous");
+  if (max_q_len < 0) return fail(PA_ERR_INVALID_ARGUMENT, "max_q_len must be non-negative");
+  if (T >= (1LL << 31)) return fail(PA_ERR_UNSUPPORTED, "too many query tokens");
+  // The attention checks run on [B, max_q_len, H, D] descriptors of the packed
+  // q/out (shape and type checks only; rows are addressed through cu_seqlens_q).
+  const int64_t mq = std::max<int64_t>(max_q_len, 1);
+  pa_tensor_t q4 = {q->data, q->dtype, 4, {B, mq, q->shape[1], q->shape[2]},
+                    {mq * q->shape[1] * q->shape[2], q->shape[1] * q->shape[2], q->shape[2], 1}};
+  pa_tensor_t o4 = q4;
+  o4.data = out->data;
+  o4.dtype = out->dtype;
+  DecodeArgs a;
+  rc = check_args(&o4, &q4, k_cache, v_cache, block_tables, context_lens, scale, true, &a);
+  if (rc) return rc;
+  if (max_q_len == 0 || T == 0) return PA_OK;
+  return run_prefill_mfma(a, q, static_cast<const int32_t*>(cu_seqlens_q->data), T, scale, stream);
 }
 
 int pa_write_kv(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tensor_t* key,

@@ -89,6 +89,8 @@ struct PrefillParams {
   int32_t B, S, H, HKV, G, D, BS, MB;
   int32_t q_dtype, out_dtype;
   int32_t q_tiles;   // ceil(S / QBLOCK)
+  const int32_t* cu_q;  // variable-length batches: [B + 1] row offsets into [T, H, D] q/out (else null)
+  int64_t q_total;      // T (variable-length batches)
   int32_t q_split;   // q is not exactly the KV type: add a low-part product
   FastDiv bs_div;
   float qscale;      // |scale| * log2(e), or 1 when scale == 0 (always positive)

@@ -205,17 +205,33 @@ void prefill_mfma_kernel(const PrefillParams p) {
   const int b = (int)(bh / p.H);
   const int kvh = h / p.G;
 
+  // This sequence's query rows: S of them (row r at position ctx - S + r)
+  // starting at token tok0 of q/out, of which the first Sr are served.
+  // Uniform batches: S = Sr = p.S.  Variable-length batches: rows cu_q[b] ..
+  // cu_q[b+1] of the packed [T, H, D] q/out, at most p.S (the caller's
+  // max_q_len) of them served; a malformed range (negative, decreasing or
+  // past T) is treated as empty.
+  int S = p.S;
+  int64_t tok0 = (int64_t)b * p.S;
+  if (p.cu_q) {
+    const int qa = p.cu_q[b], qb = p.cu_q[b + 1];
+    const bool ok = qa >= 0 && qb >= qa && (int64_t)qb <= p.q_total;
+    S = ok ? qb - qa : 0;
+    tok0 = ok ? qa : 0;
+  }
+  const int Sr = min(S, p.S);
   const int ctx = p.context_lens[b];
   const int maxctx = p.MB * p.BS;
   const int qs0 = qt * QB;
+  if (qs0 >= Sr) return;            // no served rows of this sequence here (work-group uniform)
   const int qw0 = qs0 + wave * QW;  // this wave's first query row
   const int qrow = qw0 + n;
-  const bool live = qrow < p.S;
+  const bool live = qrow < Sr;
 
   if (ctx > maxctx) {  // context longer than the block table: poison rows that attend keys
     if (live && hh == 0) {
-      const float fillv = ctx - p.S + qrow < 0 ? 0.0f : __builtin_nanf("");
-      const int64_t orow = (((int64_t)b * p.S + qrow) * p.H + h) * D;
+      const float fillv = ctx - S + qrow < 0 ? 0.0f : __builtin_nanf("");
+      const int64_t orow = ((tok0 + qrow) * p.H + h) * D;
       for (int d = 0; d < D; ++d) store_elem(p.out, p.out_dtype, orow + d, fillv);
     }
     return;
@@ -226,19 +242,19 @@ void prefill_mfma_kernel(const PrefillParams p) {
   }
 
   // Keys the work-group's rows can see: [0, kend); this wave's rows: [0, wave_kend).
-  const int kend = min(ctx, ctx - p.S + min(qs0 + QB, p.S));
+  const int kend = min(ctx, ctx - S + min(qs0 + QB, Sr));
   const int ntiles = kend > 0 ? (kend + KB - 1) / KB : 0;
-  const int wave_last = min(qw0 + QW - 1, p.S - 1);
-  const int wave_kend = qw0 < p.S ? min(ctx, ctx - p.S + wave_last + 1) : 0;
-  const int wave_kfull = ctx - p.S + qw0 + 1;  // keys below this are visible to every row of the wave
-  const int qpos = ctx - p.S + qrow;
+  const int wave_last = min(qw0 + QW - 1, Sr - 1);
+  const int wave_kend = qw0 < Sr ? min(ctx, ctx - S + wave_last + 1) : 0;
+  const int wave_kfull = ctx - S + qw0 + 1;  // keys below this are visible to every row of the wave
+  const int qpos = ctx - S + qrow;
   const int qlim = min(qpos, kend - 1);        // last key this column may see
 
   // Q^T operand (row qrow, dims ks*16 + hh*8 .. +8) in the KV type.  The sign of
   // the scale is applied here (exactly), so the softmax scale below is positive.
   u32x4_t qf[KS], qf_lo[kSplitQ ? KS : 1];
   {
-    const int64_t qoff = (((int64_t)b * p.S + (live ? qrow : 0)) * p.H + h) * D + hh * 8;
+    const int64_t qoff = ((tok0 + (live ? qrow : 0)) * p.H + h) * D + hh * 8;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if constexpr (!kSplitQ) {
@@ -584,7 +600,7 @@ void prefill_mfma_kernel(const PrefillParams p) {
   if (!live) return;
   const bool bad = bad_from <= qpos;
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-  const int64_t orow = (((int64_t)b * p.S + qrow) * p.H + h) * D;
+  const int64_t orow = ((tok0 + qrow) * p.H + h) * D;
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll

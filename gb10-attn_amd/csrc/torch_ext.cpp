@@ -10,7 +10,8 @@
 //   choose_num_splits      kernels/paged_attn_v3.h:17
 //   paged_attention_prefill       kernels/paged_attn_prefill.h:13-15
 //   paged_attention_prefill_wmma  kernels/paged_attn_wmma.h:13-15
-// plus write_kv (the engine's KV-cache write, pa_write_kv).  As in the
+// plus paged_attention_prefill_varlen (mixed decode + prefill batches) and
+// write_kv (the engine's KV-cache write, pa_write_kv).  As in the
 // reference, inputs are made contiguous (K/V only when the kernels cannot
 // address the given strides), block tables and context lengths are cast to
 // int32, and the v3 scratch comes from the caching allocator per call.  Work
@@ -135,6 +136,19 @@ at::Tensor op_paged_attention_v3(const at::Tensor& q, const at::Tensor& k, const
   return out;
 }
 
+at::Tensor op_paged_attention_prefill_varlen(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                             const at::Tensor& bt, const at::Tensor& ctx, const at::Tensor& cu,
+                                             int64_t max_q_len, double scale) {
+  Args a = prep(q, k, v, bt, ctx, 3, "[T, H, D]");
+  at::Tensor cuq = cu.to(a.q.device(), at::kInt).contiguous();
+  c10::DeviceGuard guard(a.q.device());
+  at::Tensor out = at::empty(a.q.sizes(), a.q.options().dtype(at::kFloat));
+  pa_tensor_t o = view(out), qq = view(a.q), kk = view(a.k), vv = view(a.v), bb = view(a.bt), cc = view(a.ctx),
+              uu = view(cuq);
+  check(paged_attention_prefill_varlen(&o, &qq, &kk, &vv, &bb, &cc, &uu, max_q_len, scale, stream_of(a.q)));
+  return out;
+}
+
 int64_t op_choose_num_splits(int64_t num_seqs, int64_t num_heads, int64_t max_context) {
   const int64_t s = choose_num_splits(num_seqs, num_heads, max_context);
   TORCH_CHECK(s > 0, pa_last_error());
@@ -170,6 +184,9 @@ TORCH_LIBRARY(gb10_attn, m) {
         "Tensor context_lens, float scale) -> Tensor", &op_paged_attention_prefill);
   m.def("paged_attention_prefill_wmma(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, "
         "Tensor context_lens, float scale) -> Tensor", &op_paged_attention_prefill_wmma);
+  m.def("paged_attention_prefill_varlen(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, "
+        "Tensor context_lens, Tensor cu_seqlens_q, int max_q_len, float scale) -> Tensor",
+        &op_paged_attention_prefill_varlen);
   m.def("write_kv(Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor key, Tensor value, Tensor slot_mapping) -> ()",
         &op_write_kv);
 }

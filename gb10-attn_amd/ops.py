@@ -117,6 +117,23 @@ def paged_attention_prefill_wmma(q, k_cache, v_cache, block_tables, context_lens
                         context_lens, scale, out_dtype, out, 4, "[B, S, H, D]")
 
 
+def paged_attention_prefill_varlen(q, k_cache, v_cache, block_tables, context_lens, cu_seqlens_q,
+                                   max_q_len, scale, *, out_dtype=torch.float32, out=None):
+    """Mixed decode + prefill batch on the MFMA path: q/out packed [T, H, D],
+    sequence b's q_len_b = cu_seqlens_q[b+1] - cu_seqlens_q[b] new tokens at
+    rows cu_seqlens_q[b] .., positions context_lens[b] - q_len_b + r (causal)."""
+    q, k_cache, v_cache, block_tables, context_lens = _prep(
+        q, k_cache, v_cache, block_tables, context_lens, 3, "[T, H, D]")
+    cu = cu_seqlens_q.to(q.device, torch.int32).contiguous()
+    o = _out(q, out_dtype, out)
+    with torch.cuda.device(q.device):
+        check(lib().paged_attention_prefill_varlen(
+            C.byref(view(o)), C.byref(view(q)), C.byref(view(k_cache)), C.byref(view(v_cache)),
+            C.byref(view(block_tables)), C.byref(view(context_lens)), C.byref(view(cu)), int(max_q_len),
+            float(scale), _stream(q.device)))
+    return o
+
+
 def workspace_size(q, k_cache, block_tables, num_splits) -> int:
     """Bytes of scratch paged_attention_v3 needs (0 when no split is planned)."""
     with torch.cuda.device(q.device):

@@ -172,6 +172,22 @@ int paged_attention_prefill_wmma(pa_tensor_t* out, const pa_tensor_t* q,
                                  const pa_tensor_t* block_tables,
                                  const pa_tensor_t* context_lens, double scale, void* stream);
 
+/* Variable-length (mixed decode + prefill) batches on the MFMA path.  The
+ * reference's prefill takes q [B, S, H, D] with one S for every sequence
+ * (kernels/paged_attn_prefill.cu:62-64 trailing-chunk semantics); here
+ * sequence b brings q_len_b = cu_seqlens_q[b+1] - cu_seqlens_q[b] new tokens
+ * (1 for a decode step, a chunk for prefill), packed in q/out [T, H, D]
+ * from row cu_seqlens_q[b].  Row r of sequence b sits at position
+ * context_lens[b] - q_len_b + r and attends keys [0, that position], as in
+ * paged_attention_prefill_wmma.  cu_seqlens_q is int32 [B + 1] on the device;
+ * max_q_len must bound every q_len_b (rows past it are not written).  A
+ * sequence whose range is negative, decreasing or beyond T is skipped (its
+ * rows are not written); nothing is read out of bounds. */
+int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                                   const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                                   const pa_tensor_t* context_lens, const pa_tensor_t* cu_seqlens_q,
+                                   int64_t max_q_len, double scale, void* stream);
+
 /* KV-cache write ("reshape and cache"): token t's K and V rows, key[t] and
  * value[t] ([T, HKV, D], any non-negative token/head strides, 16-byte aligned
  * rows), go to block slot_mapping[t] / BS, row slot_mapping[t] % BS of

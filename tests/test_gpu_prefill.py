@@ -151,3 +151,67 @@ def test_mfma_prefill_scale_sign(pa, dev, scale, kv, qt):
     inp = prefill_case(2, 90, 4, 4, 64, 16, [90, 130], seed=11, kv=kv, qt=qt)
     got = pa.paged_attention_prefill_wmma(*dev_args(inp, dev), scale)
     close(to_host(got), want_of(inp, scale))
+
+
+def varlen_case(qlens, ctxs, H, HKV, D, BS, seed, kv, qt="f32"):
+    B = len(qlens)
+    inp = oracle.paged_inputs(B, 1, HKV, D, BS, ctxs, seed=seed, kv_dtype=kv)
+    T = int(sum(qlens))
+    rng = np.random.default_rng(seed + 7)
+    q = oracle.quantize(rng.standard_normal((T, H, D), dtype=np.float32), qt)
+    cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    return inp, q, oracle.to_float(q, qt), cu
+
+
+@pytest.mark.parametrize("kv,D", [("f16", 64), ("bf16", 128), ("f16", 256)])
+def test_varlen_mixed_decode_and_prefill(pa, dev, kv, D):
+    """Sequences bringing 1 (decode), 0, 37, 130 and 300 new tokens against
+    contexts of equal or larger length (chunked): each sequence's rows equal
+    the oracle's prefill of that sequence alone; decode rows equal decode."""
+    qlens = [1, 37, 0, 130, 1, 300]
+    ctxs = [700, 37, 20, 1000, 1, 333]
+    H, HKV, BS = 4, 2, 16
+    inp, q, q32, cu = varlen_case(qlens, ctxs, H, HKV, D, BS, seed=D, kv=kv, qt=kv)
+    got = to_host(pa.paged_attention_prefill_varlen(
+        to_dev(q, kv, dev), to_dev(inp["k"], kv, dev), to_dev(inp["v"], kv, dev),
+        torch.from_numpy(inp["bt"]).to(dev), torch.from_numpy(inp["ctx"]).to(dev),
+        torch.from_numpy(cu).to(dev), max(qlens), 1.0 / np.sqrt(D)))
+    for b, n in enumerate(qlens):
+        if n == 0:
+            continue
+        rows = slice(cu[b], cu[b + 1])
+        want = oracle.prefill(q32[rows][None], inp["k"], inp["v"], inp["bt"][b:b + 1], inp["ctx"][b:b + 1],
+                              1.0 / np.sqrt(D), kv)[0]
+        close(got[rows], want)
+        if n == 1:
+            close(got[rows], oracle.decode(q32[rows], inp["k"], inp["v"], inp["bt"][b:b + 1],
+                                           inp["ctx"][b:b + 1], 1.0 / np.sqrt(D), kv))
+
+
+def test_varlen_malformed_ranges_and_max_q_len(pa, dev):
+    """A decreasing range and a range past T are skipped, rows past max_q_len
+    are not written (sentinel kept), and the other sequences are unaffected."""
+    qlens = [5, 40, 10]
+    ctxs = [50, 40, 70]
+    inp, q, q32, cu = varlen_case(qlens, ctxs, 4, 4, 64, 16, seed=3, kv="f16")
+    args = (torch.from_numpy(q).to(dev), to_dev(inp["k"], "f16", dev), to_dev(inp["v"], "f16", dev),
+            torch.from_numpy(inp["bt"]).to(dev), torch.from_numpy(inp["ctx"]).to(dev))
+    T = int(cu[-1])
+    for cu_bad, max_q, good in (([0, 5, 3, 56], 40, [0]),          # sequence 1 decreasing, 2 past T (55)
+                                ([0, 5, 45, 55], 32, [0, 2])):     # sequence 1 longer than max_q_len
+        out = torch.full((T, 4, 64), 7.0, device=dev)
+        pa.paged_attention_prefill_varlen(*args, torch.tensor(cu_bad, dtype=torch.int32, device=dev), max_q,
+                                          0.125, out=out)
+        got = to_host(out)
+        for b in good:
+            rows = slice(cu[b], cu[b + 1])
+            want = oracle.prefill(q32[rows][None], inp["k"], inp["v"], inp["bt"][b:b + 1],
+                                  inp["ctx"][b:b + 1], 0.125, "f16")[0]
+            close(got[rows], want)
+        if max_q == 40:
+            assert np.all(got[5:] == 7.0)
+        else:  # the 32 served rows of sequence 1 keep their positions ctx - 40 + r
+            assert np.all(got[5 + 32:45] == 7.0)
+            want = oracle.prefill(q32[5:45][None], inp["k"], inp["v"], inp["bt"][1:2], inp["ctx"][1:2],
+                                  0.125, "f16")[0]
+            close(got[5:5 + 32], want[:32])
