@@ -58,8 +58,9 @@ class DecodeWorkload:
     """Paged decode with `pools` disjoint K/V pools, each holding every page of the batch."""
 
     def __init__(self, pa, *, B, H, HKV, D, BS, ctx, dtype, pools, seed, name, q_dtype=None,
-                 out_dtype=None, pool_tensor=None):
+                 out_dtype=None, pool_tensor=None, kv_scale=None):
         self.pa, self.name = pa, name
+        self.kv_scale = kv_scale  # quantised (FP8) cache: it holds N(0,1) / kv_scale
         self.B, self.H, self.HKV, self.D, self.BS = B, H, HKV, D, BS
         self.dtype = dtype
         dev = torch.device("cuda:0")
@@ -75,8 +76,9 @@ class DecodeWorkload:
             if pool_tensor is not None:
                 k, v = pool_tensor(p)
             else:
-                k = torch.randn((nb, BS, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
-                v = torch.randn((nb, BS, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+                inv = 1.0 / kv_scale if kv_scale else 1.0
+                k = (torch.randn((nb, BS, HKV, D), generator=g, device=dev, dtype=torch.float32) * inv).to(dtype)
+                v = (torch.randn((nb, BS, HKV, D), generator=g, device=dev, dtype=torch.float32) * inv).to(dtype)
             nbp = k.shape[0]
             perm = rng.permutation(nbp)[:nb].astype(np.int32)
             bt = np.zeros((B, self.MB), np.int32)
@@ -88,9 +90,9 @@ class DecodeWorkload:
             self.v.append(v)
             self.bt.append(torch.from_numpy(bt).to(dev))
             self.bt_host = bt if p == 0 else self.bt_host
-        qd = q_dtype or dtype
+        qd = q_dtype or (torch.float16 if kv_scale else dtype)
         self.q = torch.randn((B, H, D), generator=g, device=dev, dtype=torch.float32).to(qd)
-        self.out = torch.empty((B, H, D), device=dev, dtype=out_dtype or dtype)
+        self.out = torch.empty((B, H, D), device=dev, dtype=out_dtype or (torch.float16 if kv_scale else dtype))
         self.ctx = torch.from_numpy(self.ctx_host).to(dev)
         self.scale = 1.0 / float(np.sqrt(D))
         self.pools = pools
@@ -116,7 +118,12 @@ class DecodeWorkload:
     def launch(self, i, stream, ev_mid=None):
         a = self.args[i % self.pools]
         ws = self.ws.data_ptr()
-        if not self.split:
+        if self.kv_scale:  # one call (partition and reduce): the timed kernel includes the reduce
+            rc = self.L.paged_attention_v3_scaled(*a, self.scale, self.kv_scale, self.kv_scale, 0, ws,
+                                                  self.ws_bytes, stream)
+            if rc == 0 and ev_mid is not None:
+                ev_mid.record()
+        elif not self.split:
             rc = self.L.paged_attention_v3(*a, self.scale, 0, ws, self.ws_bytes, stream)
         else:
             rc = self.L.pa_v3_partition(*a, self.scale, 0, ws, self.ws_bytes, stream)
@@ -506,10 +513,24 @@ def make_c2(pa, pools):
                           pools=pools, seed=2, name="decode_c2")
 
 
+def make_c2_fp8(pa, pools):
+    """Config 2's geometry over an FP8 E4M3 cache (per-tensor scale 1/16)."""
+    return DecodeWorkload(pa, B=64, H=12, HKV=12, D=64, BS=16, ctx=[2048] * 64, dtype=torch.float8_e4m3fn,
+                          pools=pools, seed=2, name="decode_c2_fp8", kv_scale=1.0 / 16)
+
+
 def make_c3(pa, pools):
     ctx = np.random.default_rng(3).integers(1024, 32769, 32)
     return DecodeWorkload(pa, B=32, H=32, HKV=8, D=128, BS=16, ctx=ctx, dtype=torch.bfloat16,
                           pools=pools, seed=3, name="decode_c3")
+
+
+def make_c3_fp8(pa, pools):
+    """Config 3 over an FP8 E4M3 cache (bf16 q; per-tensor scale 1/16)."""
+    ctx = np.random.default_rng(3).integers(1024, 32769, 32)
+    return DecodeWorkload(pa, B=32, H=32, HKV=8, D=128, BS=16, ctx=ctx, dtype=torch.float8_e4m3fn,
+                          pools=pools, seed=3, name="decode_c3_fp8", kv_scale=1.0 / 16, q_dtype=torch.bfloat16,
+                          out_dtype=torch.bfloat16)
 
 
 def make_c5(pa):
@@ -562,7 +583,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--pools", type=int, default=6, help="rotated KV pools (config 2)")
     ap.add_argument("--workload", default="decode_c2",
-                    choices=["decode_c2", "decode_c3", "decode_c5", "prefill_c4a", "prefill_c4b",
+                    choices=["decode_c2", "decode_c3", "decode_c5", "decode_c2_fp8", "decode_c3_fp8",
+                             "prefill_c4a", "prefill_c4b",
                              "write_kv_c4a", "write_kv_c4b", "call_overhead", "mixed_c2", "copy_calib"],
                     help="with --only: run just this workload's kernel loop (for profiling)")
     ap.add_argument("--only", action="store_true", help="time only --workload, print its record")
@@ -607,6 +629,8 @@ def main():
             print(json.dumps(write_record(work, args.steps, args.warmup)), flush=True)
         else:
             work = {"decode_c2": lambda: make_c2(pa, args.pools), "decode_c3": lambda: make_c3(pa, 2),
+                    "decode_c2_fp8": lambda: make_c2_fp8(pa, args.pools),
+                    "decode_c3_fp8": lambda: make_c3_fp8(pa, 2),
                     "decode_c5": lambda: make_c5(pa)}[w]()
             print(json.dumps(decode_record(work, args.steps, args.warmup)[2]), flush=True)
         return
@@ -645,7 +669,8 @@ def main():
 
     also = []
     if not args.no_also:
-        for make in (lambda: make_c3(pa, 2), lambda: make_c5(pa)):
+        for make in (lambda: make_c3(pa, 2), lambda: make_c5(pa), lambda: make_c2_fp8(pa, args.pools),
+                     lambda: make_c3_fp8(pa, 2)):
             w = make()
             log(f"bench: {w.name}")
             also.append(decode_record(w, max(20, args.steps // 4), 5)[2])

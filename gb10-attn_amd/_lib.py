@@ -17,12 +17,13 @@ PA_ERR_UNSUPPORTED = 2
 PA_ERR_WORKSPACE = 3
 PA_ERR_HIP = 4
 
-DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_F64, DTYPE_I32, DTYPE_I64 = range(6)
+DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_F64, DTYPE_I32, DTYPE_I64, DTYPE_FP8 = range(7)
 
 # Every symbol include/pagedattn.h declares.
 EXPORTS = (
     "pa_abi_version", "pa_last_error", "paged_attention", "paged_attention_v2",
-    "paged_attention_v3", "paged_attention_v3_workspace_size", "pa_v3_partition", "pa_v3_reduce",
+    "paged_attention_v3", "paged_attention_v3_scaled", "paged_attention_v3_workspace_size",
+    "pa_v3_partition", "pa_v3_reduce",
     "choose_num_splits", "choose_num_splits_for", "pa_plan_partitions",
     "paged_attention_prefill", "paged_attention_prefill_wmma", "paged_attention_prefill_varlen",
     "pa_write_kv",
@@ -79,6 +80,8 @@ def lib() -> C.CDLL:
         f = getattr(L, n)
         f.restype = C.c_int
         f.argtypes = six + [C.c_double, i64, P, sz, P]
+    L.paged_attention_v3_scaled.restype = C.c_int
+    L.paged_attention_v3_scaled.argtypes = six + [C.c_double, C.c_double, C.c_double, i64, P, sz, P]
     L.pa_v3_reduce.restype = C.c_int
     L.pa_v3_reduce.argtypes = [T, T, T, T, T, i64, P, sz, P]
     L.paged_attention_v3_workspace_size.restype = sz

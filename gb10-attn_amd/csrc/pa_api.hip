@@ -23,6 +23,7 @@ hipError_t launch_decode_f16(const DecodeParams& p, int gc, hipStream_t stream);
 hipError_t launch_decode_bf16(const DecodeParams& p, int gc, hipStream_t stream);
 hipError_t launch_decode_f32(const DecodeParams& p, int gc, hipStream_t stream);
 hipError_t launch_decode_f64(const DecodeParams& p, int gc, hipStream_t stream);
+hipError_t launch_decode_fp8(const DecodeParams& p, int gc, hipStream_t stream);
 
 hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int gc, hipStream_t stream) {
   switch (kv_dtype) {
@@ -30,6 +31,7 @@ hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int gc, hipStream_
     case kBF16: return launch_decode_bf16(p, gc, stream);
     case kF32: return launch_decode_f32(p, gc, stream);
     case kF64: return launch_decode_f64(p, gc, stream);
+    case kFP8: return launch_decode_fp8(p, gc, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -56,6 +58,7 @@ int dtype_bytes(int dt) {
     case kF32: case kI32: return 4;
     case kF16: case kBF16: return 2;
     case kF64: case kI64: return 8;
+    case kFP8: return 1;
     default: return 0;
   }
 }
@@ -68,6 +71,7 @@ const char* dtype_name(int dt) {
     case kF64: return "float64";
     case kI32: return "int32";
     case kI64: return "int64";
+    case kFP8: return "float8_e4m3fn";
     default: return "unknown";
   }
 }
@@ -164,8 +168,9 @@ int check_args(const pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* 
     return fail(PA_ERR_INVALID_ARGUMENT, "q must be float32, float16 or bfloat16 (got %s)", dtype_name(q->dtype));
   if (out->dtype != kF32 && out->dtype != kF16 && out->dtype != kBF16)
     return fail(PA_ERR_INVALID_ARGUMENT, "out must be float32, float16 or bfloat16 (got %s)", dtype_name(out->dtype));
-  if (k->dtype != kF32 && k->dtype != kF16 && k->dtype != kBF16 && k->dtype != kF64)
-    return fail(PA_ERR_INVALID_ARGUMENT, "k_cache must be float32, float16, bfloat16 or float64 (got %s)", dtype_name(k->dtype));
+  if (k->dtype != kF32 && k->dtype != kF16 && k->dtype != kBF16 && k->dtype != kF64 && k->dtype != kFP8)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "k_cache must be float32, float16, bfloat16, float64 or float8_e4m3fn (got %s)", dtype_name(k->dtype));
   if (v->dtype != k->dtype) return fail(PA_ERR_INVALID_ARGUMENT, "v_cache must have the dtype of k_cache");
   if (bt->dtype != kI32) return fail(PA_ERR_INVALID_ARGUMENT, "block_tables must be int32");
   if (ctx->dtype != kI32) return fail(PA_ERR_INVALID_ARGUMENT, "context_lens must be int32");
@@ -233,6 +238,7 @@ int check_args(const pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* 
   p.out_dtype = out->dtype;
   p.bs_div = make_fastdiv((uint32_t)BS);
   p.qscale = (float)(scale * 1.4426950408889634);
+  p.vscale = 1.0f;
   a->kv_dtype = k->dtype;
   a->gc = decode_heads_per_wg(p.G);
   p.head_chunks = (p.G + a->gc - 1) / a->gc;
@@ -306,10 +312,17 @@ enum V3Phase { kBoth = 3, kPartition = 1, kReduce = 2 };
 
 int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const pa_tensor_t* v,
            const pa_tensor_t* bt, const pa_tensor_t* ctx, double scale, int64_t num_splits,
-           void* ws, size_t ws_bytes, void* stream, int phases) {
+           void* ws, size_t ws_bytes, void* stream, int phases, double k_scale = 1.0,
+           double v_scale = 1.0) {
   DecodeArgs a;
   int rc = check_args(out, q, k, v, bt, ctx, scale, false, &a);
   if (rc) return rc;
+  if (!std::isfinite(k_scale) || !std::isfinite(v_scale))
+    return fail(PA_ERR_INVALID_ARGUMENT, "k_scale and v_scale must be finite");
+  // Dequantisation scales of the cache (FP8): k_scale joins the softmax
+  // scale, v_scale multiplies the weighted V sum.
+  a.p.qscale = (float)(scale * k_scale * 1.4426950408889634);
+  a.p.vscale = (float)v_scale;
   if ((int64_t)a.p.B * a.p.H == 0) return PA_OK;
   Plan plan;
   if ((rc = make_plan(a.p, a.gc, num_splits, &plan))) return rc;
@@ -459,6 +472,14 @@ int paged_attention_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t
                        void* workspace, size_t workspace_bytes, void* stream) {
   return run_v3(out, q, k_cache, v_cache, block_tables, context_lens, scale, num_splits, workspace,
                 workspace_bytes, stream, kBoth);
+}
+
+int paged_attention_v3_scaled(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                              const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                              const pa_tensor_t* context_lens, double scale, double k_scale, double v_scale,
+                              int64_t num_splits, void* workspace, size_t workspace_bytes, void* stream) {
+  return run_v3(out, q, k_cache, v_cache, block_tables, context_lens, scale, num_splits, workspace,
+                workspace_bytes, stream, kBoth, k_scale, v_scale);
 }
 
 int pa_v3_partition(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,

@@ -6,7 +6,7 @@
 
 namespace pa {
 
-enum Dtype : int32_t { kF32 = 0, kF16 = 1, kBF16 = 2, kF64 = 3, kI32 = 4, kI64 = 5 };
+enum Dtype : int32_t { kF32 = 0, kF16 = 1, kBF16 = 2, kF64 = 3, kI32 = 4, kI64 = 5, kFP8 = 6 };
 
 constexpr float kNegBig = -3.0e38f;          // empty-softmax sentinel (kernels/paged_attn_v3.cu:21)
 constexpr float kLog2e = 1.4426950408889634f;
@@ -60,7 +60,8 @@ struct DecodeParams {
   int32_t part_tokens;  // > 0: fixed partition length; 0: chunk = ceil(ctx / parts)
   int32_t direct;       // 1: one partition, every WG writes the normalised output
   FastDiv bs_div;
-  float qscale;         // scale * log2(e): scores come out in log2 units
+  float qscale;         // scale * k_scale * log2(e): scores come out in log2 units
+  float vscale;         // v_scale (FP8 caches): applied to the weighted V sum
 };
 
 struct ReduceParams {

@@ -7,9 +7,9 @@
 // (the reference reads it once per query head, kernels/paged_attn_v3.cu:63).
 //
 // Gather.  A K (or V) row of one token is D * sizeof(KV) contiguous bytes.
-// LPT = D * sizeof(KV) / 16 consecutive lanes read it with one 16-byte load
-// each, so one global_load_dwordx4 instruction fetches TPI = 64 / LPT whole
-// rows (e.g. 8 rows of 128 B for D=64 fp16).  Physical addresses follow
+// LPT = D / VEC consecutive lanes read it, VEC elements each (one 16-byte
+// load; 8 bytes for FP8), so one load instruction fetches TPI = 64 / LPT
+// whole rows (e.g. 8 rows of 128 B for D=64 fp16).  Physical addresses follow
 // kernels/paged_attn_v3.cu:87-89 -- block id from the block table, then
 // block/token/head strides -- computed in 64 bits.
 //
@@ -49,13 +49,24 @@
 
 namespace pa {
 
+template <typename KV, typename = void>
+struct requires_ni : std::false_type {};
+template <typename KV>
+struct requires_ni<KV, std::void_t<decltype(KV::kNI)>> : std::true_type {};
+
+template <typename KV>
+constexpr int kni() {
+  if constexpr (requires_ni<KV>::value) return KV::kNI > 0 ? KV::kNI : PA_DECODE_NI;
+  return PA_DECODE_NI;
+}
+
 template <typename KV, int D>
 struct DecodeShape {
   static constexpr int VEC = KV::kVec;         // elements per lane per load
   static constexpr int LPT = D / VEC;          // lanes per token row
   static_assert(LPT >= 1 && LPT <= 64 && (LPT & (LPT - 1)) == 0, "unsupported D/KV combination");
   static constexpr int TPI = 64 / LPT;         // token rows per load instruction
-  static constexpr int NI = PA_DECODE_NI;      // K (and V) loads per lane per tile
+  static constexpr int NI = kni<KV>();         // K (and V) loads per lane per tile
   static constexpr int TT = NI * TPI;          // tokens per wave tile
 };
 
@@ -163,7 +174,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodePara
   // One wave tile in flight: raw K/V rows of NI tokens per lane and which of
   // them are live (inside the partition, on a page with a valid block id).
   struct Tile {
-    u32x4_t k[NI], v[NI];
+    typename KV::Raw k[NI], v[NI];
     uint32_t live;
   };
 
@@ -190,8 +201,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodePara
       bad |= (val[i] && !okb) ? 1 : 0;
       const uint32_t bb = okb ? (uint32_t)blk[i] : 0u;
       const uint32_t oo = okb ? (uint32_t)off[i] : 0u;
-      T.k[i] = load16<PA_DECODE_NT>(kbase, (uint64_t)bb * k_sb + (oo * k_st + lane_off));
-      T.v[i] = load16<PA_DECODE_NT>(vbase, (uint64_t)bb * v_sb + (oo * v_st + lane_off));
+      T.k[i] = load_raw<KV, PA_DECODE_NT>(kbase, (uint64_t)bb * k_sb + (oo * k_st + lane_off));
+      T.v[i] = load_raw<KV, PA_DECODE_NT>(vbase, (uint64_t)bb * v_sb + (oo * v_st + lane_off));
       live |= (val[i] && okb) ? (1u << i) : 0u;
     }
     T.live = live;
@@ -228,8 +239,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodePara
       const uint32_t use = okb ? 1u : 0u;
       const uint64_t rk = (uint64_t)((uint32_t)blk * use) * k_sb + (uint32_t)off0[i] * use * k_st;
       const uint64_t rv = (uint64_t)((uint32_t)blk * use) * v_sb + (uint32_t)off0[i] * use * v_st;
-      T.k[i] = load16<PA_DECODE_NT>(kbase + rk, lane_row_k);
-      T.v[i] = load16<PA_DECODE_NT>(vbase + rv, lane_row_v);
+      T.k[i] = load_raw<KV, PA_DECODE_NT>(kbase + rk, lane_row_k);
+      T.v[i] = load_raw<KV, PA_DECODE_NT>(vbase + rv, lane_row_v);
       live |= (okb && ti + slot < ct1) ? (1u << i) : 0u;
     }
     T.live = live;
@@ -384,10 +395,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodePara
     const int h = kvh * p.G + g0 + g;
     if (final_here) {
       store_elem(p.out, p.out_dtype, ((int64_t)z * p.H + h) * D + d,
-                 bad ? __builtin_nanf("") : A / L);
+                 bad ? __builtin_nanf("") : A * p.vscale / L);
     } else {
       const int64_t pidx = ((int64_t)b * p.H + h) * p.parts + part;
-      p.ws_acc[pidx * D + d] = A;
+      p.ws_acc[pidx * D + d] = A * p.vscale;
       if (d == 0) {
         p.ws_m[pidx] = M;
         p.ws_l[pidx] = bad ? __builtin_nanf("") : L;

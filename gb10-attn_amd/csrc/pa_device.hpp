@@ -2,6 +2,8 @@
 // DPP lane reductions, dtype-generic loads/stores.
 #pragma once
 
+#include <type_traits>
+
 #include "pa_common.hpp"
 
 namespace pa {
@@ -9,12 +11,15 @@ namespace pa {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------- KV types --
-// Each KV storage type is read 16 bytes per lane (one global_load_dwordx4)
-// and widened to fp32 in registers.
+// Each KV storage type is read 16 bytes per lane (one global_load_dwordx4;
+// FP8: 8 bytes) and widened to fp32 in registers.
 
 struct KvF16 {
+  using Raw = u32x4_t;
   static constexpr int kBytes = 2;
   static constexpr int kVec = 8;
   static constexpr int kCode = kF16;
@@ -26,6 +31,7 @@ struct KvF16 {
 };
 
 struct KvBF16 {
+  using Raw = u32x4_t;
   static constexpr int kBytes = 2;
   static constexpr int kVec = 8;
   static constexpr int kCode = kBF16;
@@ -39,6 +45,7 @@ struct KvBF16 {
 };
 
 struct KvF32 {
+  using Raw = u32x4_t;
   static constexpr int kBytes = 4;
   static constexpr int kVec = 4;
   static constexpr int kCode = kF32;
@@ -52,6 +59,7 @@ struct KvF32 {
 };
 
 struct KvF64 {
+  using Raw = u32x4_t;
   static constexpr int kBytes = 8;
   static constexpr int kVec = 2;
   static constexpr int kCode = kF64;
@@ -63,9 +71,46 @@ struct KvF64 {
   }
 };
 
+// OCP FP8 E4M3 ("e4m3fn": no infinities, S.1111.111 = NaN); v_cvt_pk_f32_fp8
+// widens two at a time (exact: every code is an fp32 value).  PA_FP8_WIDE
+// selects 16-byte lane loads (16 elements per lane) over 8-byte ones.
+#ifndef PA_FP8_WIDE
+#define PA_FP8_WIDE 0
+#endif
+#ifndef PA_FP8_NI
+#define PA_FP8_NI 0
+#endif
+struct KvFP8 {
+  static constexpr int kBytes = 1;
+  static constexpr int kVec = PA_FP8_WIDE ? 16 : 8;
+  static constexpr int kCode = kFP8;
+  static constexpr int kNI = PA_FP8_NI;  // loads per lane per tile (0: the default)
+  using Raw = typename std::conditional<PA_FP8_WIDE, u32x4_t, u32x2_t>::type;
+  __device__ static inline void widen(const Raw& r, float (&o)[kVec]) {
+#pragma unroll
+    for (int w = 0; w < kVec / 4; ++w) {
+      const float2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)r[w], false);
+      const float2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)r[w], true);
+      o[4 * w] = lo[0];
+      o[4 * w + 1] = lo[1];
+      o[4 * w + 2] = hi[0];
+      o[4 * w + 3] = hi[1];
+    }
+  }
+};
+
 template <int NT = 0>
 __device__ inline u32x4_t load16(const void* base, int64_t byte_off) {
   const u32x4_t* ptr = reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(base) + byte_off);
+  if constexpr (NT) return __builtin_nontemporal_load(ptr);
+  return *ptr;
+}
+
+// One lane's raw K/V load of a KV type (16 bytes, or 8 for FP8).
+template <typename KV, int NT = 0>
+__device__ inline typename KV::Raw load_raw(const void* base, int64_t byte_off) {
+  using Raw = typename KV::Raw;
+  const Raw* ptr = reinterpret_cast<const Raw*>(reinterpret_cast<const char*>(base) + byte_off);
   if constexpr (NT) return __builtin_nontemporal_load(ptr);
   return *ptr;
 }

@@ -33,6 +33,7 @@ int pa_dtype(at::ScalarType t) {
     case at::kDouble: return PA_DTYPE_F64;
     case at::kInt: return PA_DTYPE_I32;
     case at::kLong: return PA_DTYPE_I64;
+    case at::kFloat8_e4m3fn: return PA_DTYPE_FP8_E4M3;
     default: TORCH_CHECK(false, "unsupported dtype ", t);
   }
   return -1;
@@ -136,6 +137,26 @@ at::Tensor op_paged_attention_v3(const at::Tensor& q, const at::Tensor& k, const
   return out;
 }
 
+at::Tensor op_paged_attention_v3_scaled(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                        const at::Tensor& bt, const at::Tensor& ctx, double scale,
+                                        int64_t num_splits, double k_scale, double v_scale) {
+  Args a = prep(q, k, v, bt, ctx, 3, "[B, H, D]");
+  c10::DeviceGuard guard(a.q.device());
+  at::Tensor out = at::empty(a.q.sizes(), a.q.options().dtype(at::kFloat));
+  pa_tensor_t o = view(out), qq = view(a.q), kk = view(a.k), vv = view(a.v), bb = view(a.bt), cc = view(a.ctx);
+  const size_t ws = paged_attention_v3_workspace_size(&qq, &kk, &bb, num_splits);
+  TORCH_CHECK(ws != (size_t)-1, pa_last_error());
+  at::Tensor scratch;
+  void* wp = nullptr;
+  if (ws > 0) {
+    scratch = at::empty({(int64_t)ws + 256}, a.q.options().dtype(at::kByte));
+    wp = reinterpret_cast<void*>((reinterpret_cast<uintptr_t>(scratch.data_ptr()) + 255) & ~uintptr_t(255));
+  }
+  check(paged_attention_v3_scaled(&o, &qq, &kk, &vv, &bb, &cc, scale, k_scale, v_scale, num_splits, wp, ws,
+                                  stream_of(a.q)));
+  return out;
+}
+
 at::Tensor op_paged_attention_prefill_varlen(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                                              const at::Tensor& bt, const at::Tensor& ctx, const at::Tensor& cu,
                                              int64_t max_q_len, double scale) {
@@ -179,6 +200,9 @@ TORCH_LIBRARY(gb10_attn, m) {
         "Tensor context_lens, float scale) -> Tensor", &op_paged_attention_v2);
   m.def("paged_attention_v3(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, "
         "Tensor context_lens, float scale, int num_splits) -> Tensor", &op_paged_attention_v3);
+  m.def("paged_attention_v3_scaled(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, "
+        "Tensor context_lens, float scale, int num_splits, float k_scale, float v_scale) -> Tensor",
+        &op_paged_attention_v3_scaled);
   m.def("choose_num_splits(int num_seqs, int num_heads, int max_context) -> int", &op_choose_num_splits);
   m.def("paged_attention_prefill(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, "
         "Tensor context_lens, float scale) -> Tensor", &op_paged_attention_prefill);

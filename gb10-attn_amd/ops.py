@@ -8,7 +8,8 @@ does).  As in the reference, the output is a new fp32 tensor by default;
 stream of q's device; nothing synchronises.
 
 Differences from the reference, all in the direction of accepting more:
-K/V may be fp16, bf16, fp32 or fp64 for every decode entry point and bf16 for
+K/V may be fp16, bf16, fp32, fp64 or float8_e4m3fn (with k_scale/v_scale on
+v3) for every decode entry point and bf16 for
 the matrix-core prefill; q may be fp32, fp16 or bf16; K/V may be strided
 views (e.g. one layer of a larger pool) without a copy.  Rows of a sequence
 with context_lens <= 0 are zeros; context_lens beyond the block table or
@@ -23,12 +24,13 @@ import ctypes as C
 
 import torch
 
-from ._lib import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, DTYPE_F64, DTYPE_I32, DTYPE_I64, PaTensor,
-                   check, last_error, lib)
+from ._lib import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, DTYPE_F64, DTYPE_FP8, DTYPE_I32, DTYPE_I64,
+                   PaTensor, check, last_error, lib)
 
 _DT = {
     torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16,
     torch.float64: DTYPE_F64, torch.int32: DTYPE_I32, torch.int64: DTYPE_I64,
+    torch.float8_e4m3fn: DTYPE_FP8,
 }
 
 
@@ -145,11 +147,13 @@ def workspace_size(q, k_cache, block_tables, num_splits) -> int:
 
 
 def paged_attention_v3(q, k_cache, v_cache, block_tables, context_lens, scale, num_splits, *,
-                       out_dtype=torch.float32, out=None, workspace=None):
+                       out_dtype=torch.float32, out=None, workspace=None, k_scale=1.0, v_scale=1.0):
     """kernels/paged_attn_v3.h:13-16 -- context-split decode + separate LSE reduce.
 
     num_splits > 0 cuts each sequence exactly as the reference does;
-    num_splits <= 0 lets the library plan the split from the CU count."""
+    num_splits <= 0 lets the library plan the split from the CU count.
+    k_scale / v_scale dequantise a scaled cache (e.g. torch.float8_e4m3fn):
+    attention runs on k_cache * k_scale and v_cache * v_scale."""
     q, k_cache, v_cache, block_tables, context_lens = _prep(
         q, k_cache, v_cache, block_tables, context_lens, 3, "[B, H, D]")
     o = _out(q, out_dtype, out)
@@ -157,10 +161,16 @@ def paged_attention_v3(q, k_cache, v_cache, block_tables, context_lens, scale, n
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
     with torch.cuda.device(q.device):
-        check(lib().paged_attention_v3(
-            C.byref(view(o)), C.byref(view(q)), C.byref(view(k_cache)), C.byref(view(v_cache)),
-            C.byref(view(block_tables)), C.byref(view(context_lens)), float(scale),
-            int(num_splits), workspace.data_ptr(), workspace.numel(), _stream(q.device)))
+        if k_scale == 1.0 and v_scale == 1.0:
+            check(lib().paged_attention_v3(
+                C.byref(view(o)), C.byref(view(q)), C.byref(view(k_cache)), C.byref(view(v_cache)),
+                C.byref(view(block_tables)), C.byref(view(context_lens)), float(scale),
+                int(num_splits), workspace.data_ptr(), workspace.numel(), _stream(q.device)))
+        else:
+            check(lib().paged_attention_v3_scaled(
+                C.byref(view(o)), C.byref(view(q)), C.byref(view(k_cache)), C.byref(view(v_cache)),
+                C.byref(view(block_tables)), C.byref(view(context_lens)), float(scale), float(k_scale),
+                float(v_scale), int(num_splits), workspace.data_ptr(), workspace.numel(), _stream(q.device)))
     return o
 
 

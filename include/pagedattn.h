@@ -25,7 +25,9 @@
  *   prefill q / out     [B, S, H, D]
  *   k_cache / v_cache   [NB, BS, HKV, D]   (any element strides; the last dim
  *                                           must be contiguous; all offsets are
- *                                           computed in 64 bits)
+ *                                           computed in 64 bits).  Decode paths
+ *                                           take fp32, fp16, bf16, fp64 or FP8
+ *                                           E4M3; the MFMA prefill fp16 / bf16.
  *   block_tables        int32 [B, MB]      (row stride may exceed MB)
  *   context_lens        int32 [B]
  * Token j of sequence b, KV head kvh, lives at
@@ -58,7 +60,8 @@ typedef enum pa_dtype {
   PA_DTYPE_BF16 = 2,
   PA_DTYPE_F64 = 3,
   PA_DTYPE_I32 = 4,
-  PA_DTYPE_I64 = 5
+  PA_DTYPE_I64 = 5,
+  PA_DTYPE_FP8_E4M3 = 6  /* OCP FP8 E4M3 (torch.float8_e4m3fn): KV caches of the decode paths */
 } pa_dtype_t;
 
 typedef enum pa_status {
@@ -171,6 +174,18 @@ int paged_attention_prefill_wmma(pa_tensor_t* out, const pa_tensor_t* q,
                                  const pa_tensor_t* k_cache, const pa_tensor_t* v_cache,
                                  const pa_tensor_t* block_tables,
                                  const pa_tensor_t* context_lens, double scale, void* stream);
+
+/* paged_attention_v3 over a quantised KV cache: the cache holds K / k_scale
+ * and V / v_scale (per-tensor scales, e.g. a float8_e4m3fn cache), and the
+ * result is computed on K = k_cache * k_scale, V = v_cache * v_scale.  Any
+ * decode KV type is accepted; with k_scale = v_scale = 1 it is
+ * paged_attention_v3.  No reference counterpart: the reference has no FP8
+ * cache (docs/REPORT.md:270 lists it as not done).  Workspace as for
+ * paged_attention_v3 (same split plan). */
+int paged_attention_v3_scaled(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                              const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                              const pa_tensor_t* context_lens, double scale, double k_scale, double v_scale,
+                              int64_t num_splits, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Variable-length (mixed decode + prefill) batches on the MFMA path.  The
  * reference's prefill takes q [B, S, H, D] with one S for every sequence

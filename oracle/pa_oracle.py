@@ -22,7 +22,7 @@ SIMD_PATH = HERE / "liboracle_simd.so"
 REF_PATH = HERE / "_ref" / "libgb10_ref.so"
 
 DTYPE_CODE = {"f32": 0, "f16": 1, "bf16": 2, "f64": 3}
-NP_OF = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "f64": np.float64}
+NP_OF = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "f64": np.float64, "fp8": np.uint8}
 
 
 class _KV(C.Structure):
@@ -148,8 +148,42 @@ def bf16_decode(bits) -> np.ndarray:
     return out
 
 
+def fp8_decode(bits) -> np.ndarray:
+    """OCP FP8 E4M3 ("e4m3fn") bits (uint8) -> float32, from the format
+    definition: sign, 4-bit exponent (bias 7), 3-bit mantissa; exponent 0 is
+    subnormal (m/8 * 2^-6); S.1111.111 is NaN; there are no infinities."""
+    b = np.asarray(bits, np.uint8).astype(np.int64)
+    e, m = (b >> 3) & 15, b & 7
+    mag = np.where(e == 0, m * 2.0 ** -9, (8 + m) * 2.0 ** (e - 10))
+    mag = np.where((e == 15) & (m == 7), np.nan, mag)
+    return np.where(b >> 7 == 1, -mag, mag).astype(np.float32)
+
+
+_FP8_POS = None
+
+
+def fp8_encode(x) -> np.ndarray:
+    """float32 -> FP8 E4M3 bits, round to nearest (ties to the even code),
+    saturating at +-448 (the largest finite value), as FP8 KV-cache
+    quantisers do (torch's cast instead gives NaN past 464); NaN -> 0x7f."""
+    global _FP8_POS
+    if _FP8_POS is None:
+        _FP8_POS = fp8_decode(np.arange(127, dtype=np.uint8)).astype(np.float64)  # codes 0..126, increasing
+    x = np.asarray(x, np.float32).astype(np.float64)
+    a = np.minimum(np.abs(x), 448.0)
+    hi = np.clip(np.searchsorted(_FP8_POS, a, side="left"), 0, 126)
+    lo = np.clip(hi - 1, 0, 126)
+    dlo, dhi = a - _FP8_POS[lo], _FP8_POS[hi] - a
+    code = np.where(dlo < dhi, lo, np.where(dhi < dlo, hi, np.where(lo % 2 == 0, lo, hi)))
+    code = np.where(a == _FP8_POS[hi], hi, code)
+    out = (code | np.where(np.signbit(x), 128, 0)).astype(np.uint8)
+    return np.where(np.isnan(x), np.uint8(0x7F), out)
+
+
 def to_float(a: np.ndarray, dtype: str) -> np.ndarray:
     """Exact float32 values of an array stored as `dtype`."""
+    if dtype == "fp8":
+        return fp8_decode(a)
     if dtype == "bf16":
         return bf16_decode(a)
     if dtype == "f16":
@@ -160,6 +194,8 @@ def to_float(a: np.ndarray, dtype: str) -> np.ndarray:
 def quantize(x: np.ndarray, dtype: str) -> np.ndarray:
     """Round float32 data to storage `dtype` (numpy container per NP_OF)."""
     x = np.asarray(x, np.float32)
+    if dtype == "fp8":
+        return fp8_encode(x)
     if dtype == "bf16":
         return bf16_encode(x)
     if dtype == "f16":

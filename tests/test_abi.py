@@ -74,7 +74,7 @@ ENTRY_EXTRA = {
     (dict(H=6, HKV=4), 1, "n_head must be divisible by n_kv_head"),
     (dict(D=96), 2, "unsupported head_dim 96"),
     (dict(D=48), 2, "unsupported head_dim 48"),
-    (dict(kvdt=I32), 1, "k_cache must be float32, float16, bfloat16 or float64"),
+    (dict(kvdt=I32), 1, "k_cache must be float32, float16, bfloat16, float64 or float8_e4m3fn"),
     (dict(qdt=F64), 1, "q must be float32, float16 or bfloat16"),
     (dict(odt=I64), 1, "out must be float32, float16 or bfloat16"),
     (dict(kvdt=F64, D=256), 2, "float64 KV caches support head_dim <= 128"),

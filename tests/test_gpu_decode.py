@@ -292,3 +292,66 @@ def test_partials_match_oracle_split(pa, dev):
     f = np.exp(m_nat - pm)
     close((l * f)[live], pl[live], atol=1e-4, rtol=1e-4)
     close((acc * f[..., None])[live], pacc[live], atol=1e-3, rtol=1e-3)
+
+
+def fp8_case(B, H, HKV, D, BS, ctx, *, seed, k_scale, v_scale):
+    """FP8 E4M3 caches holding K / k_scale and V / v_scale, and the oracle's
+    inputs: the dequantised values (fp8_decode(code) * scale) as fp32."""
+    inp = decode_case(B, H, HKV, D, BS, ctx, seed=seed, kv="f32", q="f32")
+    k8 = oracle.fp8_encode(inp["k"] / np.float32(k_scale))
+    v8 = oracle.fp8_encode(inp["v"] / np.float32(v_scale))
+    kf = oracle.fp8_decode(k8) * np.float32(k_scale)
+    vf = oracle.fp8_decode(v8) * np.float32(v_scale)
+    return inp, k8, v8, kf, vf
+
+
+def fp8_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).view(torch.float8_e4m3fn).to(dev)
+
+
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("H,HKV", [(4, 4), (8, 2), (16, 2)])
+def test_fp8_decode_v3_scaled(pa, dev, D, H, HKV):
+    inp, k8, v8, kf, vf = fp8_case(3, H, HKV, D, 16, [300, 17, 1100], seed=D + H, k_scale=0.05, v_scale=0.02)
+    q = torch.from_numpy(inp["q_f32"]).to(dev)
+    bt, ctx = torch.from_numpy(inp["bt"]).to(dev), torch.from_numpy(inp["ctx"]).to(dev)
+    want = oracle.decode(inp["q_f32"], kf, vf, inp["bt"], inp["ctx"], 0.1, "f32")
+    for splits in (0, 1, 5):
+        got = pa.paged_attention_v3(q, fp8_dev(k8, dev), fp8_dev(v8, dev), bt, ctx, 0.1, splits,
+                                    k_scale=0.05, v_scale=0.02)
+        close(to_host(got), want)
+    got = pa.torch_ops().paged_attention_v3_scaled(q, fp8_dev(k8, dev), fp8_dev(v8, dev), bt, ctx, 0.1, 0,
+                                                   0.05, 0.02)
+    close(to_host(got), want)
+
+
+def test_fp8_unscaled_entry_points(pa, dev):
+    """v1, v2 and the fp32 prefill read an FP8 cache as is (scale 1)."""
+    inp, k8, v8, kf, vf = fp8_case(2, 8, 4, 64, 16, [90, 200], seed=5, k_scale=1.0, v_scale=1.0)
+    q = torch.from_numpy(inp["q_f32"]).to(dev)
+    args = (fp8_dev(k8, dev), fp8_dev(v8, dev), torch.from_numpy(inp["bt"]).to(dev),
+            torch.from_numpy(inp["ctx"]).to(dev))
+    want = oracle.decode(inp["q_f32"], kf, vf, inp["bt"], inp["ctx"], 0.125, "f32")
+    close(to_host(pa.paged_attention(q, *args, 0.125)), want)
+    close(to_host(pa.paged_attention_v2(q, *args, 0.125)), want)
+    got = to_host(pa.paged_attention_prefill(q[:, None], *args, 0.125))[:, 0]
+    close(got, want)
+    with pytest.raises(RuntimeError, match="the MFMA path needs an fp16 or bf16 KV cache"):
+        pa.paged_attention_prefill_wmma(q[:, None], *args, 0.125)
+
+
+def test_fp8_every_code_through_the_kernel(pa, dev):
+    """V rows cycle through all 254 finite E4M3 codes, K is constant (uniform
+    weights): the output is the mean of the decoded codes the row sees, so a
+    wrong hardware widening of any code shows."""
+    NB, BS, HKV, D = 16, 16, 1, 64
+    codes = np.array([c for c in range(256) if c & 0x7F != 0x7F], np.uint8)
+    v8 = np.resize(codes, NB * BS * HKV * D).reshape(NB, BS, HKV, D)
+    k8 = np.full_like(v8, 0x38)  # 1.0
+    bt = np.arange(NB, dtype=np.int32)[None]
+    ctx = np.array([NB * BS], np.int32)
+    q = np.ones((1, 1, D), np.float32)
+    want = oracle.decode(q, oracle.fp8_decode(k8), oracle.fp8_decode(v8), bt, ctx, 0.01, "f32")
+    got = pa.paged_attention_v3(torch.from_numpy(q).to(dev), fp8_dev(k8, dev), fp8_dev(v8, dev),
+                                torch.from_numpy(bt).to(dev), torch.from_numpy(ctx).to(dev), 0.01, 3)
+    close(to_host(got), want, atol=1e-4, rtol=1e-5)

@@ -417,3 +417,23 @@ def test_write_kv_oracle_pins():
     bits = rng.integers(0, 1 << 16, (T, HKV, D)).astype(np.uint16)
     oracle.write_kv(kc, vc, bits, bits, slots, "bf16", "bf16")
     assert np.array_equal(kc[slots[0] // BS, slots[0] % BS], bits[0])
+
+
+def test_fp8_codec_matches_torch():
+    """fp8_decode over all 256 E4M3 codes equals torch.float8_e4m3fn's widening
+    (an independent implementation), NaN included; fp8_encode equals torch's
+    round-to-nearest-even narrowing on random data and every halfway point."""
+    codes = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = oracle.fp8_decode(codes)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(got[~np.isnan(got)], ref[~np.isnan(ref)])
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(20000).astype(np.float32) * s for s in (1e-3, 0.1, 1.0, 30.0, 200.0)])
+    finite = np.sort(np.unique(ref[np.isfinite(ref) & (ref >= 0)]))
+    mids = ((finite[1:].astype(np.float64) + finite[:-1]) / 2).astype(np.float32)
+    x = np.concatenate([x, mids, -mids, finite, -finite])
+    x = x[np.abs(x) <= 464.0]  # past 464 torch gives NaN; the encoder saturates (checked below)
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(oracle.fp8_encode(x), want)
+    assert list(oracle.fp8_encode(np.float32([470, 1e6, -500, np.nan]))) == [0x7E, 0x7E, 0xFE, 0x7F]
