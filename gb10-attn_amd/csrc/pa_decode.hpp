@@ -46,6 +46,9 @@
 #ifndef PA_DECODE_PRIO
 #define PA_DECODE_PRIO 0
 #endif
+#ifndef PA_DECODE_MFMA
+#define PA_DECODE_MFMA 1  // GQA groups of >= 4 heads on the matrix-core kernel
+#endif
 
 namespace pa {
 

@@ -355,3 +355,28 @@ def test_fp8_every_code_through_the_kernel(pa, dev):
     got = pa.paged_attention_v3(torch.from_numpy(q).to(dev), fp8_dev(k8, dev), fp8_dev(v8, dev),
                                 torch.from_numpy(bt).to(dev), torch.from_numpy(ctx).to(dev), 0.01, 3)
     close(to_host(got), want, atol=1e-4, rtol=1e-5)
+
+
+@pytest.mark.parametrize("kv,qt", [("f16", "f32"), ("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16")])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("G,BS", [(4, 16), (8, 32), (16, 16)])
+def test_gqa_matrix_core_path(pa, dev, kv, qt, D, G, BS):
+    """GQA groups of >= 8 heads with 16-aligned pages run on the MFMA decode
+    kernel (groups of 4 on the VALU kernel): ragged contexts (partial last tiles), a context long enough for the
+    planner to split it (partials + reduce), v1 (one partition), and rows poisoned
+    by an invalid block id or a context past the table."""
+    HKV = 2
+    inp = decode_case(4, HKV * G, HKV, D, BS, [37, 3000, 1, 701], seed=D + G, kv=kv, q=qt, extra_blocks=2)
+    q, k, v, bt, ctx = dev_inputs(inp, dev)
+    want = oracle.decode(inp["q_f32"], inp["k"], inp["v"], inp["bt"], inp["ctx"], 0.09, kv)
+    close(to_host(pa.paged_attention_v3(q, k, v, bt, ctx, 0.09, 0)), want)
+    close(to_host(pa.paged_attention(q, k, v, bt, ctx, 0.09)), want)
+    bt2 = inp["bt"].copy()
+    bt2[3, 5] = -7
+    ctx2 = inp["ctx"].copy()
+    ctx2[2] = bt2.shape[1] * BS + 1
+    want2 = oracle.decode(inp["q_f32"], inp["k"], inp["v"], bt2, ctx2, 0.09, kv)
+    got2 = to_host(pa.paged_attention_v3(q, k, v, torch.from_numpy(bt2).to(dev), torch.from_numpy(ctx2).to(dev),
+                                         0.09, 0))
+    assert np.array_equal(np.isnan(got2), np.isnan(want2)) and np.isnan(want2[2]).all() and np.isnan(want2[3]).all()
+    close(got2, want2)
