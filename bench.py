@@ -14,8 +14,10 @@ kernel's duration is measured with HIP events recorded on the launch stream
 around each partition launch inside the same timed loop.
 
 Also measured (the "also" list): config 3 (GQA bf16 ragged decode), config 5
-(77 GB pool, 64-bit offsets), configs 4a/4b (MFMA causal prefill, TFLOP/s),
-and the KV-cache write of the 4a/4b prompts into their pools (GB/s).
+(77 GB pool, 64-bit offsets), configs 2 and 3 over FP8 E4M3 caches, a GQA
+group of 8 heads (matrix-core decode kernel), configs 4a/4b (MFMA causal
+prefill, TFLOP/s), the KV-cache write of the 4a/4b prompts into their pools
+(GB/s), a mixed decode + prefill batch, and the per-call host cost.
 
 cpu_baseline: the reference's own scalar cpu_reference
 (rocm/hip/paged_attn_v1_hip.cpp:104-141, built into oracle/_ref), one thread,
@@ -533,6 +535,12 @@ def make_c3_fp8(pa, pools):
                           out_dtype=torch.bfloat16)
 
 
+def make_gqa8(pa, pools):
+    """GQA group of 8 (Llama-3-70B-like heads: HQ=64, HKV=8, D=128), bf16, ctx 8192: the matrix-core decode path."""
+    return DecodeWorkload(pa, B=32, H=64, HKV=8, D=128, BS=16, ctx=[8192] * 32, dtype=torch.bfloat16,
+                          pools=pools, seed=8, name="decode_gqa8")
+
+
 def make_c5(pa):
     """[12 layers, 2, 131072 blocks, 16, 12, 64] fp16 pool (77.3 GB), decode on layer 11."""
     dev = torch.device("cuda:0")
@@ -583,7 +591,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--pools", type=int, default=6, help="rotated KV pools (config 2)")
     ap.add_argument("--workload", default="decode_c2",
-                    choices=["decode_c2", "decode_c3", "decode_c5", "decode_c2_fp8", "decode_c3_fp8",
+                    choices=["decode_c2", "decode_c3", "decode_c5", "decode_c2_fp8", "decode_c3_fp8", "decode_gqa8",
                              "prefill_c4a", "prefill_c4b",
                              "write_kv_c4a", "write_kv_c4b", "call_overhead", "mixed_c2", "copy_calib"],
                     help="with --only: run just this workload's kernel loop (for profiling)")
@@ -631,6 +639,7 @@ def main():
             work = {"decode_c2": lambda: make_c2(pa, args.pools), "decode_c3": lambda: make_c3(pa, 2),
                     "decode_c2_fp8": lambda: make_c2_fp8(pa, args.pools),
                     "decode_c3_fp8": lambda: make_c3_fp8(pa, 2),
+                    "decode_gqa8": lambda: make_gqa8(pa, 2),
                     "decode_c5": lambda: make_c5(pa)}[w]()
             print(json.dumps(decode_record(work, args.steps, args.warmup)[2]), flush=True)
         return
@@ -670,7 +679,7 @@ def main():
     also = []
     if not args.no_also:
         for make in (lambda: make_c3(pa, 2), lambda: make_c5(pa), lambda: make_c2_fp8(pa, args.pools),
-                     lambda: make_c3_fp8(pa, 2)):
+                     lambda: make_c3_fp8(pa, 2), lambda: make_gqa8(pa, 2)):
             w = make()
             log(f"bench: {w.name}")
             also.append(decode_record(w, max(20, args.steps // 4), 5)[2])
