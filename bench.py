@@ -340,27 +340,34 @@ def call_overhead(pa, calls=3000):
             **res}
 
 
+REPEATS = 3
+
+
 def timed(work, steps, warmup):
     """(ms per step, mean dominant-kernel ms).
 
-    ms per step: `steps` back-to-back launches after `warmup`, bracketed by a
-    synchronize and one pair of HIP events on the launch stream.  Dominant
-    kernel: a second pass of `steps` launches with an event pair recorded on
-    the launch stream around each partition launch (events between launches
-    add a small gap, so they are kept out of the first pass)."""
+    ms per step: the median over REPEATS repeats of `steps` back-to-back
+    launches after `warmup`, each repeat bracketed by a synchronize and one
+    pair of HIP events on the launch stream.  Dominant kernel: a further pass
+    of `steps` launches with an event pair recorded on the launch stream
+    around each partition launch (events between launches add a small gap, so
+    they are kept out of the step timing)."""
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
     for i in range(warmup):
         work.launch(i, sp)
     torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for i in range(steps):
-        work.launch(warmup + i, sp)
-    t1.record(stream)
-    torch.cuda.synchronize()
-    per_step = t0.elapsed_time(t1) / steps
+    reps = []
+    for r in range(REPEATS):
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for i in range(steps):
+            work.launch(warmup + r * steps + i, sp)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        reps.append(t0.elapsed_time(t1) / steps)
+    per_step = float(np.median(reps))
 
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     mids = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
@@ -368,7 +375,7 @@ def timed(work, steps, warmup):
     split = getattr(work, "split", False)
     for i in range(steps):
         starts[i].record(stream)
-        work.launch(warmup + steps + i, sp, mids[i] if split else None)
+        work.launch(warmup + REPEATS * steps + i, sp, mids[i] if split else None)
         ends[i].record(stream)
     torch.cuda.synchronize()
     kern = [starts[i].elapsed_time(mids[i] if split else ends[i]) for i in range(steps)]
@@ -654,6 +661,7 @@ def main():
     line = {
         "metric": METRIC, "value": rec["value"], "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "timing": f"median of {REPEATS} repeats of {args.steps} steps",
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic N(0,1), seeded; random-permutation block tables",
         "config": {"workload": "decode_c2", "batch": 64, "context_len": 2048, "heads": 12,
