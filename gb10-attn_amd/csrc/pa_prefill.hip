@@ -410,16 +410,21 @@ void prefill_mfma_kernel(const PrefillParams p) {
           }
         }
       } else {
+        // Rows are substituted only at the end of the keys or on a bad block
+        // id: the zeroing selects run only when some lane of the wave has one.
+        const bool all_used = __builtin_amdgcn_ballot_w64(umask != (1u << CPT) - 1u) == 0;
 #pragma unroll
         for (int c = 0; c < CPT; ++c) {
-          const bool use = (umask >> c) & 1u;
           u32x4_t w;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const uint32_t x = vreg[c][j];
             w[j] = pack2<false>(__builtin_bit_cast(float, x << 16), __builtin_bit_cast(float, x & 0xffff0000u));
           }
-          if (!use) w = u32x4_t{0u, 0u, 0u, 0u};
+          if (!all_used) {
+            asm volatile("");
+            if (!((umask >> c) & 1u)) w = u32x4_t{0u, 0u, 0u, 0u};
+          }
           *reinterpret_cast<u32x4_t*>(dV + ((c * 4 + wave) * 64 + lane) * 8) = w;
         }
       }
@@ -457,16 +462,20 @@ void prefill_mfma_kernel(const PrefillParams p) {
           }
         }
       }
+      // Max over this lane half's keys of the column; the other half holds the
+      // column's other keys.  The two halves share m, and m only has to move
+      // when some half exceeds m + 2^8, so the cross-half max is formed only
+      // on that (rare) branch.
       float mx = -__builtin_inff();
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // the other half holds the column's other keys
-      const float mxs = mx * qscale;
-      if (__builtin_amdgcn_ballot_w64(mxs > m + kLazyRescale) != 0) {
+      const float mxh = mx * qscale;
+      if (__builtin_amdgcn_ballot_w64(mxh > m + kLazyRescale) != 0) {
         asm volatile("");  // rare: keep the O^T rescale behind the branch
+        const float mxs = fmaxf(mxh, __shfl_xor(mxh, 32, 64));
         const float mn = fmaxf(m, mxs);
         const float corr = mn == -__builtin_inff() ? 1.0f : fast_exp2(m - mn);
         m = mn;
