@@ -251,7 +251,7 @@ struct Plan {
   bool direct;
 };
 
-int make_plan(const DecodeParams& p, int gc, int64_t num_splits, Plan* plan) {
+int make_plan(const DecodeParams& p, int gc, int kv_bytes, int64_t num_splits, Plan* plan) {
   if (num_splits > 0) {
     if (num_splits > (1 << 20)) return fail(PA_ERR_INVALID_ARGUMENT, "num_splits too large");
     plan->parts = num_splits;
@@ -263,7 +263,10 @@ int make_plan(const DecodeParams& p, int gc, int64_t num_splits, Plan* plan) {
   int rc = device_cu_count(&cus);
   if (rc) return rc;
   int64_t ptok = 0, nparts = 0;
-  pa_plan_partitions(p.B, p.H, p.HKV, p.D, (int64_t)p.MB * p.BS, cus, &ptok, &nparts);
+  // Paired heads halve the work-groups per sequence: plan for HKV / 2 units.
+  const bool pairs = decode_pairs_k(p.D, kv_bytes, p.G, p.HKV, p.k_sh);
+  const int64_t hkv = pairs ? p.HKV / 2 : p.HKV;
+  pa_plan_partitions(p.B, hkv * p.G, hkv, p.D, (int64_t)p.MB * p.BS, cus, &ptok, &nparts);
   (void)gc;
   plan->parts = nparts;
   plan->part_tokens = nparts > 1 ? ptok : 0;
@@ -325,7 +328,7 @@ int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const p
   a.p.vscale = (float)v_scale;
   if ((int64_t)a.p.B * a.p.H == 0) return PA_OK;
   Plan plan;
-  if ((rc = make_plan(a.p, a.gc, num_splits, &plan))) return rc;
+  if ((rc = make_plan(a.p, a.gc, dtype_bytes(a.kv_dtype), num_splits, &plan))) return rc;
   const size_t need = workspace_bytes_for(a.p.B, a.p.H, a.p.D, plan);
   if (need > 0 && (!ws || ws_bytes < need))
     return fail(PA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need, ws ? ws_bytes : 0);
@@ -510,9 +513,11 @@ size_t paged_attention_v3_workspace_size(const pa_tensor_t* q, const pa_tensor_t
   }
   DecodeParams p;
   memset(&p, 0, sizeof(p));
-  p.B = (int)B; p.H = (int)H; p.HKV = (int)HKV; p.D = (int)D; p.BS = (int)BS; p.MB = (int)MB;
+  p.B = (int)B; p.H = (int)H; p.HKV = (int)HKV; p.G = (int)(H / HKV); p.D = (int)D; p.BS = (int)BS;
+  p.MB = (int)MB;
+  p.k_sh = k_cache->stride[2];
   Plan plan;
-  if (make_plan(p, decode_heads_per_wg((int)(H / HKV)), num_splits, &plan)) return (size_t)-1;
+  if (make_plan(p, decode_heads_per_wg(p.G), dtype_bytes(k_cache->dtype), num_splits, &plan)) return (size_t)-1;
   return workspace_bytes_for(B, H, D, plan);
 }
 

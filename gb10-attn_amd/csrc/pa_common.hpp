@@ -123,6 +123,14 @@ hipError_t launch_reduce(const ReduceParams& p, hipStream_t stream);
 hipError_t launch_prefill_mfma(const PrefillParams& p, int kv_dtype, hipStream_t stream);
 hipError_t launch_write_kv(const WriteParams& p, hipStream_t stream);
 
+// Two KV heads per decode work-group (MHA whose head rows are shorter than a
+// 128-byte line, heads contiguous in the pool).  The partition planner sees
+// only K (the workspace-size query has no V); the kernel also needs V's heads
+// contiguous, else it serves one head per work-group under the same plan.
+inline bool decode_pairs_k(int D, int kv_bytes, int G, int HKV, int64_t k_sh) {
+  return D * kv_bytes < 128 && G == 1 && HKV % 2 == 0 && k_sh == D;
+}
+
 // Heads per decode work-group for a GQA group of G query heads.
 inline int decode_heads_per_wg(int G) {
   if (G <= 1) return 1;

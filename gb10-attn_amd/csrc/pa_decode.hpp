@@ -46,6 +46,9 @@
 #ifndef PA_DECODE_PRIO
 #define PA_DECODE_PRIO 0
 #endif
+#ifndef PA_DECODE_PAIR
+#define PA_DECODE_PAIR 1  // two KV heads per work-group when a head's row is under 128 bytes
+#endif
 #ifndef PA_DECODE_MFMA
 #define PA_DECODE_MFMA 1  // GQA groups of >= 4 heads on the matrix-core kernel
 #endif
@@ -77,33 +80,43 @@ constexpr int kDecodeWaves = PA_DECODE_WAVES;
 constexpr int kDecodeThreads = 64 * kDecodeWaves;
 constexpr int kBtChunk = 256;  // block-table entries staged in LDS at a time
 
-template <typename KV, int D, int GC>
+// HP > 1 (MHA only, GC = 1): one work-group serves HP adjacent KV heads,
+// whose rows of a token are contiguous in the pool, as one row of HP * D
+// elements.  A head's row shorter than a 128-byte line (FP8 at D = 64, 16-bit
+// at D = 32) then costs whole-line requests instead of half-line ones; each
+// head keeps its own softmax (the dot product is summed over the head's
+// LPH lanes only).
+template <typename KV, int D, int GC, int HP = 1>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeParams p) {
-  using Sh = DecodeShape<KV, D>;
+  static_assert(HP == 1 || GC == 1, "head pairing serves MHA groups");
+  using Sh = DecodeShape<KV, D * HP>;
   constexpr int VEC = Sh::VEC, LPT = Sh::LPT, TPI = Sh::TPI, NI = Sh::NI, TT = Sh::TT;
+  constexpr int LPH = D / VEC;  // lanes per head's row
   constexpr int NW = kDecodeWaves;
 
   __shared__ int32_t s_bt[kBtChunk];
-  __shared__ float s_acc[NW][GC][D];
-  __shared__ float s_m[NW][GC];
-  __shared__ float s_l[NW][GC];
+  __shared__ float s_acc[NW][GC][HP * D];
+  __shared__ float s_m[NW][GC * HP];
+  __shared__ float s_l[NW][GC * HP];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int slot = lane / LPT;
   const int sub = lane % LPT;
+  const int hl = sub / LPH;   // this lane's head within the work-group's HP heads
+  const int dsub = sub % LPH;
 
   // blockIdx.x -> (z, part, kvh, hc), heads fastest: the work-groups that
   // read the other heads' rows of the same pages are dispatched together, so
   // a page's DRAM rows are open for all of them (one KV head's row of a token
   // is a 128-256 byte slice of the page's token row).
-  const int units_y = p.HKV * p.head_chunks;
+  const int units_y = p.HKV / HP * p.head_chunks;
   int id = blockIdx.x;
   const int y = id % units_y;
   id /= units_y;
   const int part = id % p.parts;
   const int z = id / p.parts;
-  const int kvh = y / p.head_chunks;
+  const int kvh = y / p.head_chunks;  // first KV head: kvh * HP
   const int hc = y - kvh * p.head_chunks;
   const int b = z / p.Sq;
   const int sq = z - b * p.Sq;
@@ -121,10 +134,11 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodePara
     // Zero rows for an empty context, NaN rows for one longer than the table.
     if (final_here && part == 0) {
       const float fillv = ctx <= 0 ? 0.0f : __builtin_nanf("");
-      for (int idx = threadIdx.x; idx < GC * D; idx += kDecodeThreads) {
-        const int g = idx / D, d = idx - (idx / D) * D;
+      for (int idx = threadIdx.x; idx < GC * HP * D; idx += kDecodeThreads) {
+        const int g = idx / (HP * D), dd = idx - g * (HP * D);
+        const int d = dd % D, hh = dd / D;
         if (g0 + g >= p.G) continue;
-        const int h = kvh * p.G + g0 + g;
+        const int h = (kvh * HP + hh) * p.G + g0 + g;
         store_elem(p.out, p.out_dtype, ((int64_t)z * p.H + h) * D + d, fillv);
       }
     }
@@ -147,8 +161,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodePara
 #pragma unroll
   for (int g = 0; g < GC; ++g) {
     const bool hv = g0 + g < p.G;
-    const int h = kvh * p.G + g0 + g;
-    const int64_t qb = ((int64_t)z * p.H + h) * D + sub * VEC;
+    const int h = (kvh * HP + hl) * p.G + g0 + g;
+    const int64_t qb = ((int64_t)z * p.H + h) * D + dsub * VEC;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) qr[g][e] = hv ? load_elem(p.q, p.q_dtype, qb + e) * p.qscale : 0.0f;
   }
@@ -166,8 +180,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodePara
   // Byte strides.  The host guarantees block and token strides (and BS times
   // the token stride) fit 32 bits, so a row address is one 64-bit
   // multiply-add on the block id plus a 32-bit in-block offset.
-  const char* kbase = static_cast<const char*>(p.k) + (int64_t)kvh * p.k_sh * KV::kBytes;
-  const char* vbase = static_cast<const char*>(p.v) + (int64_t)kvh * p.v_sh * KV::kBytes;
+  const char* kbase = static_cast<const char*>(p.k) + (int64_t)kvh * HP * p.k_sh * KV::kBytes;
+  const char* vbase = static_cast<const char*>(p.v) + (int64_t)kvh * HP * p.v_sh * KV::kBytes;
   const uint32_t k_sb = (uint32_t)(p.k_sb * KV::kBytes), k_st = (uint32_t)(p.k_st * KV::kBytes);
   const uint32_t v_sb = (uint32_t)(p.v_sb * KV::kBytes), v_st = (uint32_t)(p.v_st * KV::kBytes);
   const uint32_t lane_off = (uint32_t)(sub * VEC * KV::kBytes);
@@ -262,7 +276,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodePara
         float d = 0.0f;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) d = fmaf(qr[g][e], kf[e], d);
-        s[i][g] = group_sum<LPT>(d);
+        s[i][g] = group_sum<LPH>(d);
       }
     }
     float vf[NI][VEC];
@@ -372,30 +386,32 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodePara
 #pragma unroll
       for (int e = 0; e < VEC; ++e) s_acc[wave][g][sub * VEC + e] = acc[g][e];
   }
-  if (lane == 0) {
+  if (slot == 0 && dsub == 0) {
 #pragma unroll
     for (int g = 0; g < GC; ++g) {
-      s_m[wave][g] = m[g];
-      s_l[wave][g] = l[g];
+      s_m[wave][g * HP + hl] = m[g];
+      s_l[wave][g * HP + hl] = l[g];
     }
   }
   bad = __syncthreads_or(bad);
 
   // Combine the waves and write out.
-  for (int idx = threadIdx.x; idx < GC * D; idx += kDecodeThreads) {
-    const int g = idx / D, d = idx - (idx / D) * D;
+  for (int idx = threadIdx.x; idx < GC * HP * D; idx += kDecodeThreads) {
+    const int g = idx / (HP * D), dd = idx - g * (HP * D);
+    const int d = dd % D, hh = dd / D;
     if (g0 + g >= p.G) continue;
+    const int gh = g * HP + hh;
     float M = kNegBig;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][g]);
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][gh]);
     float L = 0.0f, A = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const float wt = fast_exp2(s_m[w][g] - M);
-      L += s_l[w][g] * wt;
-      A += s_acc[w][g][d] * wt;
+      const float wt = fast_exp2(s_m[w][gh] - M);
+      L += s_l[w][gh] * wt;
+      A += s_acc[w][g][dd] * wt;
     }
-    const int h = kvh * p.G + g0 + g;
+    const int h = (kvh * HP + hh) * p.G + g0 + g;
     if (final_here) {
       store_elem(p.out, p.out_dtype, ((int64_t)z * p.H + h) * D + d,
                  bad ? __builtin_nanf("") : A * p.vscale / L);
@@ -410,16 +426,26 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodePara
   }
 }
 
-template <typename KV, int D, int GC>
+template <typename KV, int D, int GC, int HP = 1>
 hipError_t launch_decode_dg(const DecodeParams& p, hipStream_t stream) {
-  const int64_t blocks = (int64_t)p.B * p.Sq * p.HKV * p.head_chunks * p.parts;
-  hipLaunchKernelGGL((decode_kernel<KV, D, GC>), dim3((unsigned)blocks), dim3(kDecodeThreads), 0,
+  const int64_t blocks = (int64_t)p.B * p.Sq * (p.HKV / HP) * p.head_chunks * p.parts;
+  hipLaunchKernelGGL((decode_kernel<KV, D, GC, HP>), dim3((unsigned)blocks), dim3(kDecodeThreads), 0,
                      stream, p);
   return hipGetLastError();
 }
 
+// Head pairing applies to MHA when a head's row is shorter than a 128-byte
+// line and adjacent heads' rows are contiguous (head stride = D).
+template <typename KV, int D>
+bool decode_pair_heads(const DecodeParams& p) {
+  return PA_DECODE_PAIR && decode_pairs_k(D, KV::kBytes, p.G, p.HKV, p.k_sh) && p.v_sh == D;
+}
+
 template <typename KV, int D>
 hipError_t launch_decode_d(const DecodeParams& p, int gc, hipStream_t stream) {
+  if constexpr (D * KV::kBytes < 128) {
+    if (gc == 1 && decode_pair_heads<KV, D>(p)) return launch_decode_dg<KV, D, 1, 2>(p, stream);
+  }
   switch (gc) {
     case 1: return launch_decode_dg<KV, D, 1>(p, stream);
     case 2: return launch_decode_dg<KV, D, 2>(p, stream);

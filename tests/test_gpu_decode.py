@@ -380,3 +380,56 @@ def test_gqa_matrix_core_path(pa, dev, kv, qt, D, G, BS):
                                          0.09, 0))
     assert np.array_equal(np.isnan(got2), np.isnan(want2)) and np.isnan(want2[2]).all() and np.isnan(want2[3]).all()
     close(got2, want2)
+
+
+@pytest.mark.parametrize("kind", ["fp8_d64", "fp8_d32", "f16_d32", "bf16_d32"])
+@pytest.mark.parametrize("HKV", [2, 6, 3])
+@pytest.mark.parametrize("BS", [16, 5])
+def test_head_pairing(pa, dev, kind, HKV, BS):
+    """MHA whose head rows are under 128 bytes: with an even head count and
+    contiguous heads two KV heads share a work-group (whole-line reads); odd
+    counts and strided head views take the one-head kernel.  All entry points,
+    ragged and empty contexts, split plans, the fast (BS % rows-per-load == 0)
+    and general gathers, rows poisoned by a bad block id or a context past the
+    table, and FP8 scales."""
+    D = 64 if kind == "fp8_d64" else 32
+    ctx = [0, 1, 37, 700, 2500]
+    seed = D + HKV * 7 + BS
+    if kind.startswith("fp8"):
+        inp, k8, v8, kf, vf = fp8_case(len(ctx), HKV, HKV, D, BS, ctx, seed=seed, k_scale=1.0, v_scale=1.0)
+        q = torch.from_numpy(inp["q_f32"]).to(dev)
+        k, v = fp8_dev(k8, dev), fp8_dev(v8, dev)
+        kref, vref, kvname = kf, vf, "f32"
+    else:
+        inp = decode_case(len(ctx), HKV, HKV, D, BS, ctx, seed=seed, kv=kind[:-4])
+        q, k, v, _, _ = dev_inputs(inp, dev)
+        kref, vref, kvname = inp["k"], inp["v"], inp["kv"]
+    bt, ctxd = torch.from_numpy(inp["bt"]).to(dev), torch.from_numpy(inp["ctx"]).to(dev)
+    want = oracle.decode(inp["q_f32"], kref, vref, inp["bt"], inp["ctx"], 0.15, kvname)
+    for entry in ("v1", "v2", "v3auto", "v3s1", "v3s3", "v3s64"):
+        got = to_host(run(pa, entry, q, k, v, bt, ctxd, 0.15))
+        assert np.all(got[0] == 0.0)
+        close(got, want)
+    # Heads strided by 2 * D (every other head of a wider pool): not paired.
+    k2 = torch.zeros((k.shape[0], BS, 2 * HKV, D), dtype=k.dtype, device=dev)
+    v2 = torch.zeros_like(k2)
+    k2[:, :, ::2] = k
+    v2[:, :, ::2] = v
+    close(to_host(run(pa, "v3auto", q, k2[:, :, ::2], v2[:, :, ::2], bt, ctxd, 0.15)), want)
+    # Poisoned rows.
+    bt2 = inp["bt"].copy()
+    bt2[4, 3] = -3
+    ctx2 = inp["ctx"].copy()
+    ctx2[2] = bt2.shape[1] * BS + 1
+    want2 = oracle.decode(inp["q_f32"], kref, vref, bt2, ctx2, 0.15, kvname)
+    got2 = to_host(pa.paged_attention_v3(q, k, v, torch.from_numpy(bt2).to(dev), torch.from_numpy(ctx2).to(dev),
+                                         0.15, 0))
+    assert np.isnan(got2[2]).all() and np.isnan(got2[4]).all()
+    assert np.array_equal(np.isnan(got2), np.isnan(want2))
+    close(got2, want2)
+    if kind.startswith("fp8"):  # per-tensor scales through the scaled entry
+        inp, k8, v8, kf, vf = fp8_case(len(ctx), HKV, HKV, D, BS, ctx, seed=seed, k_scale=0.05, v_scale=0.03)
+        want = oracle.decode(inp["q_f32"], kf, vf, inp["bt"], inp["ctx"], 0.15, "f32")
+        got = pa.paged_attention_v3(torch.from_numpy(inp["q_f32"]).to(dev), fp8_dev(k8, dev), fp8_dev(v8, dev),
+                                    bt, ctxd, 0.15, 0, k_scale=0.05, v_scale=0.03)
+        close(to_host(got), want)
