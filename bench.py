@@ -341,6 +341,9 @@ def call_overhead(pa, calls=3000):
 
 
 REPEATS = 3
+# The reference's published figure for config 2 (v3 split decode, B=64,
+# ctx=2048), measured on NVIDIA GB10: 231.3 GB/s = 84.7 % of its 273 GB/s.
+REF_GB10_C2_GBS = 231.3
 
 
 def timed(work, steps, warmup):
@@ -662,7 +665,13 @@ def main():
         "metric": METRIC, "value": rec["value"], "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
         "timing": f"median of {REPEATS} repeats of {args.steps} steps",
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": round(rec["value"] / REF_GB10_C2_GBS, 2),
+        "baseline": {"value": REF_GB10_C2_GBS, "unit": "GB/s", "frac_of_its_peak": 0.847,
+                     "what": "reference v3 split decode, B=64 ctx=2048 fp16 (this config), on NVIDIA GB10 "
+                             "(273 GB/s LPDDR5X): different hardware, compare frac_of_peak",
+                     "source": "docs/REPORT.md:124"},
+        "dtype": "f16",
         "data": "synthetic N(0,1), seeded; random-permutation block tables",
         "config": {"workload": "decode_c2", "batch": 64, "context_len": 2048, "heads": 12,
                    "kv_heads": 12, "head_dim": 64, "block_size": 16, "kv_dtype": "f16",
