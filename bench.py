@@ -9,9 +9,12 @@ above the 256 MB Infinity Cache and every K/V byte comes from HBM.
 A step is one paged_attention_v3 call (partition kernel, plus the reduce
 kernel when the plan splits) on one pool, inputs resident in HBM.  `value` is
 algorithmic bytes per step (K and V of every live token once, plus q, out,
-block tables and context lengths) / measured time per step.  The dominant
-kernel's duration is measured with HIP events recorded on the launch stream
-around each partition launch inside the same timed loop.
+block tables and context lengths) / measured time per step (median of
+three timed loops, each bracketed by HIP events on the launch stream).  The
+dominant kernel's average duration (`roofline.achieved`): when the step is
+that one kernel, the same loops; when the plan splits, HIP events on the
+launch stream around each partition launch, in loops alternating with the
+step loops.
 
 Also measured (the "also" list): config 3 (GQA bf16 ragged decode), config 5
 (77 GB pool, 64-bit offsets), configs 2 and 3 over FP8 E4M3 caches, a GQA
@@ -224,7 +227,7 @@ WRITE_CFG = {
 
 
 def write_record(work, steps, warmup):
-    ms, kms = timed(work, steps, warmup)
+    ms, kms, _ = timed(work, steps, warmup)
     gbs = work.bytes / (kms * 1e-3) / 1e9
     return {
         "workload": work.name, "value": round(gbs, 1), "unit": "GB/s",
@@ -280,11 +283,11 @@ class MixedWorkload:
 
 def mixed_record(pa, steps, warmup):
     w = MixedWorkload(pa)
-    ms, _ = timed(w, steps, warmup)
+    ms, _, _ = timed(w, steps, warmup)
 
     class Split:
         launch = w.launch_split
-    ms_split, _ = timed(Split(), steps, warmup)
+    ms_split, _, _ = timed(Split(), steps, warmup)
     return {"workload": w.name, "unit": "ms per step",
             "case": f"{w.nd} decode rows + {w.npf} x {w.chunk}-token prefill chunks, ctx 2048, H=12 D=64 fp16",
             "varlen_ms": round(ms, 5), "split_ms": round(ms_split, 5),
@@ -347,42 +350,50 @@ REF_GB10_C2_GBS = 231.3
 
 
 def timed(work, steps, warmup):
-    """(ms per step, mean dominant-kernel ms).
+    """(ms per step, mean dominant-kernel ms, per-repeat step ms).
 
-    ms per step: the median over REPEATS repeats of `steps` back-to-back
-    launches after `warmup`, each repeat bracketed by a synchronize and one
-    pair of HIP events on the launch stream.  Dominant kernel: a further pass
-    of `steps` launches with an event pair recorded on the launch stream
-    around each partition launch (events between launches add a small gap, so
-    they are kept out of the step timing)."""
+    REPEATS rounds after `warmup` launches; each round is a step loop
+    (`steps` back-to-back launches bracketed by a synchronize and one pair of
+    HIP events on the launch stream) followed by a kernel loop (`steps`
+    launches with an event pair on the launch stream around each partition
+    launch; events between launches add a small gap, so they stay out of
+    the step loops).  ms per step is the median over the step loops.  The
+    dominant kernel's time: when a step is that one kernel, the step loops
+    already measure it (events over the timed region / launches; a pair
+    around every launch would add ~2 us to a 66 us kernel); otherwise the
+    mean over every bracketed launch.  Step and kernel loops alternate so
+    both sample the same span: this device runs the first work of a process
+    a few percent faster than what follows."""
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
     for i in range(warmup):
         work.launch(i, sp)
     torch.cuda.synchronize()
-    reps = []
+    split = getattr(work, "split", False)
+    reps, kern = [], []
+    n = warmup
     for r in range(REPEATS):
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
         t0.record(stream)
         for i in range(steps):
-            work.launch(warmup + r * steps + i, sp)
+            work.launch(n + i, sp)
         t1.record(stream)
         torch.cuda.synchronize()
         reps.append(t0.elapsed_time(t1) / steps)
-    per_step = float(np.median(reps))
-
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    mids = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    split = getattr(work, "split", False)
-    for i in range(steps):
-        starts[i].record(stream)
-        work.launch(warmup + REPEATS * steps + i, sp, mids[i] if split else None)
-        ends[i].record(stream)
-    torch.cuda.synchronize()
-    kern = [starts[i].elapsed_time(mids[i] if split else ends[i]) for i in range(steps)]
-    return per_step, float(np.mean(kern))
+        n += steps
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        mids = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        for i in range(steps):
+            starts[i].record(stream)
+            work.launch(n + i, sp, mids[i] if split else None)
+            ends[i].record(stream)
+        torch.cuda.synchronize()
+        kern += [starts[i].elapsed_time(mids[i] if split else ends[i]) for i in range(steps)]
+        n += steps
+    ms = float(np.median(reps))
+    return ms, (float(np.mean(kern)) if split else ms), [round(x, 5) for x in reps]
 
 
 def traffic_from_profiles(kernel_key):
@@ -571,11 +582,11 @@ def make_c5(pa):
 
 
 def decode_record(work, steps, warmup):
-    ms, kms = timed(work, steps, warmup)
+    ms, kms, reps = timed(work, steps, warmup)
     gbs = work.bytes / (ms * 1e-3) / 1e9
     return ms, kms, {
         "workload": work.name, "value": round(gbs, 1), "unit": "GB/s",
-        "frac_of_8TBs": round(gbs / PEAK_HBM_GBS, 4), "ms_per_step": round(ms, 5),
+        "frac_of_8TBs": round(gbs / PEAK_HBM_GBS, 4), "ms_per_step": round(ms, 5), "repeats_ms": reps,
         "kernel_ms": round(kms, 5), "tokens_per_s": round(work.B / (ms * 1e-3), 1),
         "bytes_per_step": int(work.bytes), "split": work.split,
         "pools": work.pools, "footprint_GB": round(work.footprint_gb(), 2),
@@ -583,7 +594,7 @@ def decode_record(work, steps, warmup):
 
 
 def prefill_record(work, steps, warmup):
-    ms, kms = timed(work, steps, warmup)
+    ms, kms, _ = timed(work, steps, warmup)
     tf = work.flops / (kms * 1e-3) / 1e12
     return {
         "workload": work.name, "value": round(tf, 1), "unit": "TFLOP/s",
@@ -664,7 +675,7 @@ def main():
     line = {
         "metric": METRIC, "value": rec["value"], "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
-        "timing": f"median of {REPEATS} repeats of {args.steps} steps",
+        "timing": f"median of {REPEATS} repeats of {args.steps} steps", "repeats_ms": rec["repeats_ms"],
         "higher_is_better": True, "scaling": "weak",
         "vs_baseline": round(rec["value"] / REF_GB10_C2_GBS, 2),
         "baseline": {"value": REF_GB10_C2_GBS, "unit": "GB/s", "frac_of_its_peak": 0.847,

@@ -86,8 +86,12 @@ constexpr int kBtChunk = 256;  // block-table entries staged in LDS at a time
 // at D = 32) then costs whole-line requests instead of half-line ones; each
 // head keeps its own softmax (the dot product is summed over the head's
 // LPH lanes only).
+// Groups of up to 4 heads are held to two waves per SIMD (<= 256 registers),
+// which the loads in flight need; left to itself the allocator has tipped
+// GC = 4 at D = 128 into one wave per SIMD (config 3: 415 -> 518 us).
 template <typename KV, int D, int GC, int HP = 1>
-__global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const DecodeParams p) {
+__global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(GC <= 4 ? 2 : 1)))
+void decode_kernel(const DecodeParams p) {
   static_assert(HP == 1 || GC == 1, "head pairing serves MHA groups");
   using Sh = DecodeShape<KV, D * HP>;
   constexpr int VEC = Sh::VEC, LPT = Sh::LPT, TPI = Sh::TPI, NI = Sh::NI, TT = Sh::TT;
