@@ -123,7 +123,10 @@ int device_cu_count(int* cus) {
 struct PlanKnobs {
   int64_t wgs_per_cu = 3;   // target resident work-groups per CU
   int64_t min_part = 256;   // shortest partition worth a work-group (tokens)
-  int64_t max_part = 2048;  // longest partition (bounds ragged imbalance)
+  int64_t max_part = 2048;        // longest partition (bounds ragged imbalance)
+  int64_t max_part_split = 1024;  // the same when the plan splits anyway and the VALU kernel serves
+                                  // the group: finer balance for ragged batches (config 3: +4 %); the
+                                  // matrix-core kernel (groups of 8+) amortises its set-up over 2048
 };
 
 const PlanKnobs& knobs() {
@@ -132,6 +135,7 @@ const PlanKnobs& knobs() {
     if (const char* s = getenv("PA_PLAN_WGS_PER_CU")) r.wgs_per_cu = std::max(1L, atol(s));
     if (const char* s = getenv("PA_PLAN_MIN_PART")) r.min_part = std::max(16L, atol(s));
     if (const char* s = getenv("PA_PLAN_MAX_PART")) r.max_part = std::max(16L, atol(s));
+    if (const char* s = getenv("PA_PLAN_MAX_PART_SPLIT")) r.max_part_split = std::max(16L, atol(s));
     return r;
   }();
   return k;
@@ -442,7 +446,8 @@ int pa_plan_partitions(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads
   const int64_t units = std::max<int64_t>(1, num_seqs * num_kv_heads * ((G + gc - 1) / gc));
   const int64_t target = num_compute_units * kn.wgs_per_cu;
   int64_t S = (target + units - 1) / units;                             // fill the GPU
-  S = std::max(S, (max_context + kn.max_part - 1) / kn.max_part);       // bound partition length
+  const int64_t max_part = S > 1 && gc < 8 ? kn.max_part_split : kn.max_part;
+  S = std::max(S, (max_context + max_part - 1) / max_part);             // bound partition length
   S = std::min(S, std::max<int64_t>(1, max_context / kn.min_part));     // keep partitions long
   if (S <= 1 || max_context <= 0) {
     *partition_tokens = std::max<int64_t>(max_context, 1);
