@@ -26,10 +26,10 @@
 //    more than 2^8 (probabilities stay <= 256, exact in fp16/bf16 range), so
 //    the O^T rescale is a rare wave-uniform branch instead of a per-tile
 //    multiply.  Masking runs only on tiles that cross a wave's diagonal.
-//  * Work-groups are ordered longest-first within a (sequence, head) and the
-//    (sequence, head) ranges are laid out so that consecutive ranges land on
-//    the same XCD (work-group i runs on XCD i mod 8), keeping a head's K/V
-//    pages in one L2.
+//  * Work-groups are ordered by query block, longest first, across all
+//    (sequence, head) pairs.  (Grouping one (sequence, head)'s blocks on one
+//    XCD, for L2 reuse, put three blocks of the same length on each CU when
+//    all work-groups are resident: config 4a ran 22 % slower.)
 //
 // Semantics follow kernels/paged_attn_wmma.cu:80-205: query row r of the
 // chunk sits at ctx - S + r and sees keys [0, ctx - S + r]; accumulation and
@@ -117,6 +117,7 @@ constexpr int kPfThreads = 256;   // 4 waves
 constexpr int kPfBtStage = 1024;  // block-table entries staged in LDS
 constexpr float kLazyRescale = 8.0f;  // raise the running max only past 2^8
 
+
 // How a tile's P.V product is formed.
 enum PvMode : int {
   kPvDirect = 0,   // V tile loaded straight into LDS; P and V in fp16
@@ -193,13 +194,14 @@ void prefill_mfma_kernel(const PrefillParams p) {
   const int n = lane & 31;   // query column of this lane (S^T, O^T) / key row (K operand)
   const int hh = lane >> 5;  // lane half: k-slot block of the operands
 
-  // Work-group -> (b, h, query block): XCD-contiguous, longest block first.
+  // Work-group -> (b, h, query block): query blocks longest first across all
+  // (sequence, head) pairs (the block index is the slow one), so every CU's
+  // resident work-groups mix long and short blocks.
   const int nq = p.q_tiles;
-  const int64_t total = (int64_t)p.B * p.H * nq;
-  int64_t x = blockIdx.x;
-  if ((total & 7) == 0) x = (x & 7) * (total >> 3) + (x >> 3);
-  const int qt = nq - 1 - (int)(x % nq);
-  const int64_t bh = x / nq;
+  const int64_t nbh = (int64_t)p.B * p.H;
+  const int64_t x = blockIdx.x;
+  const int qt = nq - 1 - (int)(x / nbh);
+  const int64_t bh = x % nbh;
   const int h = (int)(bh % p.H);
   const int b = (int)(bh / p.H);
   const int kvh = h / p.G;
