@@ -593,12 +593,47 @@ def decode_record(work, steps, warmup):
     }
 
 
+_GEMM_REF = {}
+
+
+def library_gemm_tflops(dtype, n=8192, reps=10):
+    """Dense n x n x n product of N(0,1) operands through torch.matmul (the
+    ROCm GEMM library) on this device: what its matrix cores sustain on
+    random data in this run, for reading the prefill fraction against.
+    Sustained MFMA throughput depends on the operand values (random operands
+    draw more power than constant ones and the clock drops), so the published
+    dense peak is not reachable with real data."""
+    if dtype in _GEMM_REF:
+        return _GEMM_REF[dtype]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    a = torch.randn((n, n), generator=g, device="cuda", dtype=torch.float32).to(dtype)
+    b = torch.randn((n, n), generator=g, device="cuda", dtype=torch.float32).to(dtype)
+    for _ in range(3):
+        c = torch.matmul(a, b)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        c = torch.matmul(a, b)
+    t1.record()
+    torch.cuda.synchronize()
+    tf = 2.0 * n ** 3 * reps / (t0.elapsed_time(t1) * 1e-3) / 1e12
+    del a, b, c
+    torch.cuda.empty_cache()
+    _GEMM_REF[dtype] = round(tf, 1)
+    return _GEMM_REF[dtype]
+
+
 def prefill_record(work, steps, warmup):
     ms, kms, _ = timed(work, steps, warmup)
     tf = work.flops / (kms * 1e-3) / 1e12
+    gemm = library_gemm_tflops(work.dtype)
     return {
         "workload": work.name, "value": round(tf, 1), "unit": "TFLOP/s",
-        "frac_of_mfma_peak": round(tf / PEAK_MFMA_TFLOPS, 4), "ms_per_step": round(ms, 5),
+        "frac_of_mfma_peak": round(tf / PEAK_MFMA_TFLOPS, 4),
+        "library_gemm_tflops": gemm, "frac_of_library_gemm": round(tf / gemm, 4),
+        "ms_per_step": round(ms, 5),
         "kernel_ms": round(kms, 5), "flops_per_step": work.flops,
         "prompt_tokens_per_s": round(work.q.shape[0] * work.q.shape[1] / (ms * 1e-3), 1),
         "dtype": str(work.dtype).replace("torch.", ""),
