@@ -165,10 +165,15 @@ void decode_kernel(const DecodeParams p) {
 #pragma unroll
   for (int g = 0; g < GC; ++g) {
     const bool hv = g0 + g < p.G;
-    const int h = (kvh * HP + hl) * p.G + g0 + g;
+    const int h = (kvh * HP + hl) * p.G + g0 + (hv ? g : 0);
     const int64_t qb = ((int64_t)z * p.H + h) * D + dsub * VEC;
+    load_elems<VEC>(p.q, p.q_dtype, qb, qr[g]);
+  }
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) qr[g][e] = hv ? load_elem(p.q, p.q_dtype, qb + e) * p.qscale : 0.0f;
+  for (int g = 0; g < GC; ++g) {
+    const bool hv = g0 + g < p.G;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) qr[g][e] = hv ? qr[g][e] * p.qscale : 0.0f;
   }
 
   float m[GC], l[GC], acc[GC][VEC];

@@ -166,13 +166,16 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(const DecodeParams p) 
   u32x4_t qf[KS], qlo[KS];
   {
     const int64_t qb = ((int64_t)z * p.H + kvh * p.G + g0 + (qlive ? col : 0)) * D + kg * 8;
+    float xq[KS][8];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) load_elems<8>(p.q, p.q_dtype, qb + 32 * ks, xq[ks]);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       uint32_t w[4], wl[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float x0 = qlive ? load_elem(p.q, p.q_dtype, qb + 32 * ks + 2 * j) : 0.0f;
-        const float x1 = qlive ? load_elem(p.q, p.q_dtype, qb + 32 * ks + 2 * j + 1) : 0.0f;
+        const float x0 = qlive ? xq[ks][2 * j] : 0.0f;
+        const float x1 = qlive ? xq[ks][2 * j + 1] : 0.0f;
         w[j] = pack2m<kBf16>(x0, x1);
         const float2_t r = unpack2m<kBf16>(w[j]);
         wl[j] = pack2m<kBf16>(x0 - r[0], x1 - r[1]);

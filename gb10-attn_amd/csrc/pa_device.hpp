@@ -127,6 +127,88 @@ __device__ inline float load_elem(const void* p, int dtype, int64_t i) {
   }
 }
 
+// N consecutive elements p[i .. i+N) as fp32, i a multiple of N.  All loads
+// of the row are issued before any is used, with the widest vector the base
+// alignment allows (the branch is uniform: it depends on p and dtype only).
+// A kernel's prologue then costs one memory round trip for its q row instead
+// of one per element, which matters when the loads queue behind other
+// work-groups' K/V streams.
+typedef _Float16 f16x2v_t __attribute__((ext_vector_type(2)));
+template <int N>
+__device__ inline void load_elems(const void* p, int dtype, int64_t i, float (&o)[N]) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  if (dtype == kF32) {
+    const float* f = static_cast<const float*>(p) + i;
+    if constexpr (N % 4 == 0) {
+      if ((a & 15) == 0) {
+        float4_t v[N / 4];
+#pragma unroll
+        for (int k = 0; k < N / 4; ++k) v[k] = reinterpret_cast<const float4_t*>(f)[k];
+#pragma unroll
+        for (int k = 0; k < N / 4; ++k) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[4 * k + e] = v[k][e];
+        }
+        return;
+      }
+    }
+    if constexpr (N % 2 == 0) {
+      if ((a & 7) == 0) {
+        float2_t v[N / 2];
+#pragma unroll
+        for (int k = 0; k < N / 2; ++k) v[k] = reinterpret_cast<const float2_t*>(f)[k];
+#pragma unroll
+        for (int k = 0; k < N / 2; ++k) {
+          o[2 * k] = v[k][0];
+          o[2 * k + 1] = v[k][1];
+        }
+        return;
+      }
+    }
+  } else if (dtype == kF16 || dtype == kBF16) {
+    const bool bf = dtype == kBF16;
+    const uint16_t* h = static_cast<const uint16_t*>(p) + i;
+    auto widen2 = [&](uint32_t w, float& x0, float& x1) {
+      if (bf) {
+        x0 = __builtin_bit_cast(float, w << 16);
+        x1 = __builtin_bit_cast(float, w & 0xffff0000u);
+      } else {
+        const f16x2v_t hv = __builtin_bit_cast(f16x2v_t, w);
+        x0 = (float)hv[0];
+        x1 = (float)hv[1];
+      }
+    };
+    if constexpr (N % 8 == 0) {
+      if ((a & 15) == 0) {
+        u32x4_t v[N / 8];
+#pragma unroll
+        for (int k = 0; k < N / 8; ++k) v[k] = reinterpret_cast<const u32x4_t*>(h)[k];
+#pragma unroll
+        for (int k = 0; k < N / 8; ++k) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) widen2(v[k][w], o[8 * k + 2 * w], o[8 * k + 2 * w + 1]);
+        }
+        return;
+      }
+    }
+    if constexpr (N % 4 == 0) {
+      if ((a & 7) == 0) {
+        u32x2_t v[N / 4];
+#pragma unroll
+        for (int k = 0; k < N / 4; ++k) v[k] = reinterpret_cast<const u32x2_t*>(h)[k];
+#pragma unroll
+        for (int k = 0; k < N / 4; ++k) {
+#pragma unroll
+          for (int w = 0; w < 2; ++w) widen2(v[k][w], o[4 * k + 2 * w], o[4 * k + 2 * w + 1]);
+        }
+        return;
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < N; ++e) o[e] = load_elem(p, dtype, i + e);
+}
+
 // fp32 -> bf16 with round-to-nearest-even (NaN kept quiet).
 __device__ inline uint16_t f32_to_bf16_bits(float x) {
   uint32_t u = __builtin_bit_cast(uint32_t, x);

@@ -433,3 +433,22 @@ def test_head_pairing(pa, dev, kind, HKV, BS):
         got = pa.paged_attention_v3(torch.from_numpy(inp["q_f32"]).to(dev), fp8_dev(k8, dev), fp8_dev(v8, dev),
                                     bt, ctxd, 0.15, 0, k_scale=0.05, v_scale=0.03)
         close(to_host(got), want)
+
+
+@pytest.mark.parametrize("qt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("G", [1, 4, 8])
+def test_q_alignment(pa, dev, qt, G):
+    """q read at every base alignment: element offsets 0, 1, 2 and 4 into a
+    larger buffer give 16-, 2/4-, 4/8- and 8/16-byte aligned rows, covering
+    the vector and per-element load paths of the VALU and matrix-core kernels."""
+    H, D = 2 * G, 64
+    inp = decode_case(3, H, 2, D, 16, [300, 17, 96], seed=70 + G, kv="bf16", q=qt)
+    _, k, v, bt, ctx = dev_inputs(inp, dev)
+    want = want_of(inp, 0.125)
+    qd = to_dev(inp["q"], qt, dev)
+    for off in (0, 1, 2, 4):
+        buf = torch.zeros(qd.numel() + off, dtype=qd.dtype, device=dev)
+        buf[off:] = qd.reshape(-1)
+        q = buf[off:].view(qd.shape)
+        for entry in ("v1", "v3auto", "v3s7"):
+            close(to_host(run(pa, entry, q, k, v, bt, ctx, 0.125)), want)
