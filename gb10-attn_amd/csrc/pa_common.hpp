@@ -90,6 +90,7 @@ struct PrefillParams {
   int32_t B, S, H, HKV, G, D, BS, MB;
   int32_t q_dtype, out_dtype;
   int32_t q_tiles;   // ceil(S / QBLOCK)
+  int32_t wg_cus;    // > 0: the whole grid is resident on this many CUs (work-group order)
   const int32_t* cu_q;  // variable-length batches: [B + 1] row offsets into [T, H, D] q/out (else null)
   int64_t q_total;      // T (variable-length batches)
   int32_t q_split;   // q is not exactly the KV type: add a low-part product

@@ -42,6 +42,8 @@
 // arrive in the KV type is likewise split into hi + lo for Q.K^T.
 #include "pa_device.hpp"
 
+#include <atomic>
+
 namespace pa {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -194,12 +196,24 @@ void prefill_mfma_kernel(const PrefillParams p) {
   const int n = lane & 31;   // query column of this lane (S^T, O^T) / key row (K operand)
   const int hh = lane >> 5;  // lane half: k-slot block of the operands
 
-  // Work-group -> (b, h, query block): query blocks longest first across all
-  // (sequence, head) pairs (the block index is the slow one), so every CU's
-  // resident work-groups mix long and short blocks.
+  // Work-group -> unit (b, h, query block).  Units are numbered with the
+  // query block as the slow index, longest first across all (sequence, head)
+  // pairs.  When the grid is more than one resident wave, work-group x takes
+  // unit x: the dispatcher hands the longest remaining unit to each CU slot
+  // that frees.  When every work-group is resident at once (p.wg_cus = C
+  // CUs), the dispatcher places work-groups x, x + C, x + 2C, ... on one CU;
+  // odd generations then take their units mirrored, so each CU's units add
+  // up to about the same number of key tiles (config 4a: 27-28 per CU instead
+  // of 20-34).  The mirror keeps x mod 8 (work-groups go to the 8 XCDs round
+  // robin), so a (sequence, head) pair's blocks, which read the same keys,
+  // stay on one XCD's L2.
   const int nq = p.q_tiles;
   const int64_t nbh = (int64_t)p.B * p.H;
-  const int64_t x = blockIdx.x;
+  int64_t x = blockIdx.x;
+  if (p.wg_cus > 0) {
+    const int64_t C = p.wg_cus, g = x / C, j = x - g * C;
+    if ((g & 1) && (g + 1) * C <= nbh * nq) x = g * C + (C % 8 == 0 ? C - 8 - (j & ~(int64_t)7) + (j & 7) : C - 1 - j);
+  }
   const int qt = nq - 1 - (int)(x / nbh);
   const int64_t bh = x % nbh;
   const int h = (int)(bh % p.H);
@@ -621,18 +635,49 @@ void prefill_mfma_kernel(const PrefillParams p) {
   }
 }
 
+// CU count of the current device and resident work-groups per CU of one
+// kernel instance, cached per device; {0, 0} if unknown.
+template <typename F>
+static void residency(F kernel, std::atomic<int64_t> (&cache)[64], int64_t* cus, int64_t* per_cu) {
+  *cus = *per_cu = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return;
+  if (dev < 64) {
+    const int64_t c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *cus = c >> 8;
+      *per_cu = c & 0xff;
+      return;
+    }
+  }
+  int n = 0, k = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, kernel, kPfThreads, 0) != hipSuccess || k <= 0 ||
+      k > 0xff)
+    return;
+  if (dev < 64) cache[dev].store(((int64_t)n << 8) | k, std::memory_order_relaxed);
+  *cus = n;
+  *per_cu = k;
+}
+
+template <typename KV, int D, bool kSplitQ>
+static hipError_t launch_pf_q(const PrefillParams& p, hipStream_t stream) {
+  static std::atomic<int64_t> cache[64];
+  const auto kernel = prefill_mfma_kernel<KV, D, kSplitQ>;
+  PrefillParams q = p;
+  const int64_t units = (int64_t)q.B * q.H * q.q_tiles;
+  int64_t cus = 0, per_cu = 0;
+  residency(kernel, cache, &cus, &per_cu);
+  q.wg_cus = units > cus && units <= cus * per_cu ? (int32_t)cus : 0;  // one resident wave
+  hipLaunchKernelGGL(kernel, dim3((unsigned)units), dim3(kPfThreads), 0, stream, q);
+  return hipGetLastError();
+}
+
 template <typename KV, int D>
 static hipError_t launch_pf(const PrefillParams& p, hipStream_t stream) {
   PrefillParams q = p;
   q.q_tiles = (p.S + PfShape<D>::QB - 1) / PfShape<D>::QB;
-  const int64_t blocks = (int64_t)q.B * q.H * q.q_tiles;
-  if (p.q_split)
-    hipLaunchKernelGGL((prefill_mfma_kernel<KV, D, true>), dim3((unsigned)blocks), dim3(kPfThreads),
-                       0, stream, q);
-  else
-    hipLaunchKernelGGL((prefill_mfma_kernel<KV, D, false>), dim3((unsigned)blocks), dim3(kPfThreads),
-                       0, stream, q);
-  return hipGetLastError();
+  return p.q_split ? launch_pf_q<KV, D, true>(q, stream) : launch_pf_q<KV, D, false>(q, stream);
 }
 
 template <typename KV>
