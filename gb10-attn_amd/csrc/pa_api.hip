@@ -127,6 +127,7 @@ struct PlanKnobs {
   int64_t max_part_split = 1024;  // the same when the plan splits anyway and the VALU kernel serves
                                   // the group: finer balance for ragged batches (config 3: +4 %); the
                                   // matrix-core kernel (groups of 8+) amortises its set-up over 2048
+  int64_t pack = 0;  // > 0: KV heads per work-group for packable layouts, whatever the split
 };
 
 const PlanKnobs& knobs() {
@@ -136,6 +137,7 @@ const PlanKnobs& knobs() {
     if (const char* s = getenv("PA_PLAN_MIN_PART")) r.min_part = std::max(16L, atol(s));
     if (const char* s = getenv("PA_PLAN_MAX_PART")) r.max_part = std::max(16L, atol(s));
     if (const char* s = getenv("PA_PLAN_MAX_PART_SPLIT")) r.max_part_split = std::max(16L, atol(s));
+    if (const char* s = getenv("PA_PLAN_PACK")) r.pack = std::max(0L, atol(s));
     return r;
   }();
   return k;
@@ -253,28 +255,72 @@ struct Plan {
   int64_t parts;
   int64_t part_tokens;  // 0 = reference count mode
   bool direct;
+  int hp;  // KV heads per work-group (head packing)
 };
 
+// Head packing for a plan with `splits` partitions per (sequence, KV head):
+// the widest packing whose work-groups still fill the GPU (target resident
+// work-groups), else the narrowest one.
+int pack_for(const DecodeParams& p, int kv_bytes, int64_t splits, int cus) {
+  const int lo = decode_pack_min(p.D, kv_bytes, p.G, p.HKV, p.k_sh);
+  const int hi = decode_pack_max(p.D, kv_bytes, p.G, p.HKV, p.k_sh);
+  const int64_t target = (int64_t)cus * knobs().wgs_per_cu;
+  for (int c = hi; c > lo; c /= 2)
+    if ((int64_t)p.B * p.Sq * (p.HKV / c) * splits >= target) return c;
+  return lo;
+}
+
+// The plan of a v3 call.  An explicit split needs no device query (the
+// workspace-size query runs without one); its packing is chosen at launch
+// (hp = 0 here).
 int make_plan(const DecodeParams& p, int gc, int kv_bytes, int64_t num_splits, Plan* plan) {
+  (void)gc;
   if (num_splits > 0) {
     if (num_splits > (1 << 20)) return fail(PA_ERR_INVALID_ARGUMENT, "num_splits too large");
     plan->parts = num_splits;
     plan->part_tokens = 0;
     plan->direct = num_splits == 1;
+    plan->hp = 0;
     return PA_OK;
   }
   int cus = 0;
   int rc = device_cu_count(&cus);
   if (rc) return rc;
-  int64_t ptok = 0, nparts = 0;
-  // Paired heads halve the work-groups per sequence: plan for HKV / 2 units.
-  const bool pairs = decode_pairs_k(p.D, kv_bytes, p.G, p.HKV, p.k_sh);
-  const int64_t hkv = pairs ? p.HKV / 2 : p.HKV;
-  pa_plan_partitions(p.B, hkv * p.G, hkv, p.D, (int64_t)p.MB * p.BS, cus, &ptok, &nparts);
-  (void)gc;
+  // Auto plan: partitions for the narrowest packing, then the widest packing
+  // that needs no more partitions than that (packing divides the work-groups
+  // per sequence; a plan that must split anyway for length absorbs it).
+  const int lo = decode_pack_min(p.D, kv_bytes, p.G, p.HKV, p.k_sh);
+  const int hi = decode_pack_max(p.D, kv_bytes, p.G, p.HKV, p.k_sh);
+  const int64_t maxctx = (int64_t)p.MB * p.BS;
+  auto parts_for = [&](int c, int64_t* ptok) {
+    int64_t np = 0;
+    pa_plan_partitions(p.B, (p.HKV / c) * p.G, p.HKV / c, p.D, maxctx, cus, ptok, &np);
+    return np;
+  };
+  int64_t ptok = 0;
+  if (knobs().pack > 0) {  // fixed packing (measurement knob)
+    int c = hi;
+    while (c > lo && c > knobs().pack) c /= 2;
+    const int64_t np = parts_for(c, &ptok);
+    plan->parts = np;
+    plan->part_tokens = np > 1 ? ptok : 0;
+    plan->direct = np <= 1;
+    plan->hp = c;
+    return PA_OK;
+  }
+  const int64_t nparts = parts_for(lo, &ptok);
+  int hp = lo;
+  for (int c = hi; c > lo; c /= 2) {
+    int64_t pt = 0;
+    if (parts_for(c, &pt) == nparts && pt == ptok) {
+      hp = c;
+      break;
+    }
+  }
   plan->parts = nparts;
   plan->part_tokens = nparts > 1 ? ptok : 0;
   plan->direct = nparts <= 1;
+  plan->hp = hp;
   return PA_OK;
 }
 
@@ -311,6 +357,9 @@ int run_direct(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, con
   a.p.parts = 1;
   a.p.part_tokens = 0;
   a.p.direct = 1;
+  int cus = 0;
+  if ((rc = device_cu_count(&cus))) return rc;
+  a.p.hp = pack_for(a.p, dtype_bytes(a.kv_dtype), 1, cus);
   return hip_status(launch_decode(a.p, a.kv_dtype, a.gc, static_cast<hipStream_t>(stream)),
                     "decode kernel launch");
 }
@@ -341,6 +390,12 @@ int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const p
   a.p.parts = (int)plan.parts;
   a.p.part_tokens = (int)plan.part_tokens;
   a.p.direct = plan.direct ? 1 : 0;
+  a.p.hp = plan.hp;
+  if (a.p.hp == 0) {
+    int cus = 0;
+    if ((rc = device_cu_count(&cus))) return rc;
+    a.p.hp = pack_for(a.p, dtype_bytes(a.kv_dtype), plan.parts, cus);
+  }
   if (!plan.direct) bind_workspace(&a.p, ws, plan);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (phases & kPartition) {

@@ -59,6 +59,7 @@ struct DecodeParams {
   int32_t parts;        // partitions per (sequence, KV head) in the grid
   int32_t part_tokens;  // > 0: fixed partition length; 0: chunk = ceil(ctx / parts)
   int32_t direct;       // 1: one partition, every WG writes the normalised output
+  int32_t hp;           // KV heads per work-group (head packing, gc == 1); <= 1: one
   FastDiv bs_div;
   float qscale;         // scale * k_scale * log2(e): scores come out in log2 units
   float vscale;         // v_scale (FP8 caches): applied to the weighted V sum
@@ -124,12 +125,35 @@ hipError_t launch_reduce(const ReduceParams& p, hipStream_t stream);
 hipError_t launch_prefill_mfma(const PrefillParams& p, int kv_dtype, hipStream_t stream);
 hipError_t launch_write_kv(const WriteParams& p, hipStream_t stream);
 
-// Two KV heads per decode work-group (MHA whose head rows are shorter than a
-// 128-byte line, heads contiguous in the pool).  The partition planner sees
-// only K (the workspace-size query has no V); the kernel also needs V's heads
-// contiguous, else it serves one head per work-group under the same plan.
-inline bool decode_pairs_k(int D, int kv_bytes, int G, int HKV, int64_t k_sh) {
-  return D * kv_bytes < 128 && G == 1 && HKV % 2 == 0 && k_sh == D;
+// Head packing (MHA, heads contiguous in the pool): one decode work-group
+// serves HP adjacent KV heads, whose rows of a token are contiguous, as one
+// row of HP * D elements.  Wider contiguous reads keep more of each DRAM row
+// access useful: at B = 256, ctx 2048, fp16 D = 64 one head per work-group
+// streams 6.42 TB/s, two 6.66, four 6.80.  Rows shorter than a 128-byte line
+// are always packed (two heads at least), since a half-line request costs
+// a whole line.  The planner chooses HP per call (DecodeParams::hp); it sees
+// only K (the workspace-size query has no V), and the kernel also needs V's
+// heads contiguous, else it serves one head per work-group under the same
+// plan.
+#ifndef PA_PACK_ROW_BYTES
+#define PA_PACK_ROW_BYTES 512  // widest packed row
+#endif
+#ifndef PA_PACK_MAX
+#define PA_PACK_MAX 4  // most KV heads per work-group
+#endif
+
+// Widest packing the layout allows (1 = none).
+inline int decode_pack_max(int D, int kv_bytes, int G, int HKV, int64_t k_sh) {
+  if (G != 1 || k_sh != D) return 1;
+  int hp = 1;
+  for (int c = 2; c <= PA_PACK_MAX; c *= 2)
+    if ((int64_t)D * kv_bytes * c <= PA_PACK_ROW_BYTES && HKV % c == 0) hp = c;
+  return hp;
+}
+
+// Narrowest packing worth running: two heads when a row is under a line.
+inline int decode_pack_min(int D, int kv_bytes, int G, int HKV, int64_t k_sh) {
+  return (D * kv_bytes < 128 && decode_pack_max(D, kv_bytes, G, HKV, k_sh) >= 2) ? 2 : 1;
 }
 
 // Heads per decode work-group for a GQA group of G query heads.

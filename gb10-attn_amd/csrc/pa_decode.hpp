@@ -46,9 +46,6 @@
 #ifndef PA_DECODE_PRIO
 #define PA_DECODE_PRIO 0
 #endif
-#ifndef PA_DECODE_PAIR
-#define PA_DECODE_PAIR 1  // two KV heads per work-group when a head's row is under 128 bytes
-#endif
 #ifndef PA_DECODE_MFMA
 #define PA_DECODE_MFMA 1  // GQA groups of >= 4 heads on the matrix-core kernel
 #endif
@@ -82,10 +79,11 @@ constexpr int kBtChunk = 256;  // block-table entries staged in LDS at a time
 
 // HP > 1 (MHA only, GC = 1): one work-group serves HP adjacent KV heads,
 // whose rows of a token are contiguous in the pool, as one row of HP * D
-// elements.  A head's row shorter than a 128-byte line (FP8 at D = 64, 16-bit
-// at D = 32) then costs whole-line requests instead of half-line ones; each
-// head keeps its own softmax (the dot product is summed over the head's
-// LPH lanes only).
+// elements (up to 512 bytes).  A head's row shorter than a 128-byte line
+// (FP8 at D = 64, 16-bit at D = 32) then costs whole-line requests instead of
+// half-line ones, and longer packed rows keep more of each DRAM access
+// useful; each head keeps its own softmax (the dot product is summed over
+// the head's LPH lanes only).
 // Groups of up to 4 heads are held to two waves per SIMD (<= 256 registers),
 // which the loads in flight need; left to itself the allocator has tipped
 // GC = 4 at D = 128 into one wave per SIMD (config 3: 415 -> 518 us).
@@ -443,17 +441,16 @@ hipError_t launch_decode_dg(const DecodeParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Head pairing applies to MHA when a head's row is shorter than a 128-byte
-// line and adjacent heads' rows are contiguous (head stride = D).
-template <typename KV, int D>
-bool decode_pair_heads(const DecodeParams& p) {
-  return PA_DECODE_PAIR && decode_pairs_k(D, KV::kBytes, p.G, p.HKV, p.k_sh) && p.v_sh == D;
-}
-
 template <typename KV, int D>
 hipError_t launch_decode_d(const DecodeParams& p, int gc, hipStream_t stream) {
-  if constexpr (D * KV::kBytes < 128) {
-    if (gc == 1 && decode_pair_heads<KV, D>(p)) return launch_decode_dg<KV, D, 1, 2>(p, stream);
+  // Packed heads (the plan's choice) need K's and V's heads contiguous.
+  if (gc == 1 && p.hp > 1 && p.k_sh == D && p.v_sh == D && p.HKV % p.hp == 0) {
+    if constexpr (D * KV::kBytes * 4 <= PA_PACK_ROW_BYTES && PA_PACK_MAX >= 4) {
+      if (p.hp == 4) return launch_decode_dg<KV, D, 1, 4>(p, stream);
+    }
+    if constexpr (D * KV::kBytes * 2 <= PA_PACK_ROW_BYTES) {
+      if (p.hp == 2) return launch_decode_dg<KV, D, 1, 2>(p, stream);
+    }
   }
   switch (gc) {
     case 1: return launch_decode_dg<KV, D, 1>(p, stream);

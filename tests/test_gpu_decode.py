@@ -435,6 +435,53 @@ def test_head_pairing(pa, dev, kind, HKV, BS):
         close(to_host(got), want)
 
 
+@pytest.mark.parametrize("kind,D,HKV", [("f16", 64, 12), ("f16", 64, 6), ("bf16", 128, 4), ("fp8", 128, 8),
+                                        ("f32", 32, 4), ("bf16", 32, 8)])
+@pytest.mark.parametrize("BS", [16, 5])
+def test_head_packing_wide_rows(pa, dev, kind, D, HKV, BS):
+    """Head packing up to 512-byte rows.  The planner packs four heads (128-byte
+    rows: fp16 D=64 with 12 heads, FP8 D=128, fp32 D=32; 64-byte bf16 D=32
+    rows) or two (256-byte rows, or a head count not divisible by four) when
+    the packed work-groups still fill the GPU -- here the explicit 256-way
+    split (whose reduce also walks more than 64 partitions per row); v1, the
+    3-way split and the auto plan of this small batch keep the narrow packing.
+    Ragged and empty contexts, both gathers (BS=5 is the general one), a
+    strided V (the kernel then serves one head per work-group under the same
+    plan), and rows poisoned by a bad block id or a context past the table."""
+    ctx = [0, 1, 37, 700, 9000]
+    seed = 3 * D + HKV + BS
+    if kind == "fp8":
+        inp, k8, v8, kf, vf = fp8_case(len(ctx), HKV, HKV, D, BS, ctx, seed=seed, k_scale=1.0, v_scale=1.0)
+        q = torch.from_numpy(inp["q_f32"]).to(dev)
+        k, v = fp8_dev(k8, dev), fp8_dev(v8, dev)
+        kref, vref, kvname = kf, vf, "f32"
+    else:
+        inp = decode_case(len(ctx), HKV, HKV, D, BS, ctx, seed=seed, kv=kind)
+        q, k, v, _, _ = dev_inputs(inp, dev)
+        kref, vref, kvname = inp["k"], inp["v"], inp["kv"]
+    bt, ctxd = torch.from_numpy(inp["bt"]).to(dev), torch.from_numpy(inp["ctx"]).to(dev)
+    want = oracle.decode(inp["q_f32"], kref, vref, inp["bt"], inp["ctx"], 0.11, kvname)
+    for entry in ("v1", "v3auto", "v3s3", "v3s256"):
+        got = to_host(run(pa, entry, q, k, v, bt, ctxd, 0.11))
+        assert np.all(got[0] == 0.0)
+        close(got, want)
+    # V with heads strided by 2 * D: packing is off for this call's kernel.
+    v2 = torch.zeros((v.shape[0], BS, 2 * HKV, D), dtype=v.dtype, device=dev)
+    v2[:, :, ::2] = v
+    close(to_host(run(pa, "v3auto", q, k, v2[:, :, ::2], bt, ctxd, 0.11)), want)
+    # Poisoned rows.
+    bt2 = inp["bt"].copy()
+    bt2[4, 300] = -3
+    ctx2 = inp["ctx"].copy()
+    ctx2[2] = bt2.shape[1] * BS + 1
+    want2 = oracle.decode(inp["q_f32"], kref, vref, bt2, ctx2, 0.11, kvname)
+    for entry in ("v3auto", "v3s256"):
+        got2 = to_host(run(pa, entry, q, k, v, torch.from_numpy(bt2).to(dev), torch.from_numpy(ctx2).to(dev), 0.11))
+        assert np.isnan(got2[2]).all() and np.isnan(got2[4]).all()
+        assert np.array_equal(np.isnan(got2), np.isnan(want2))
+        close(got2, want2)
+
+
 @pytest.mark.parametrize("qt", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("G", [1, 4, 8])
 def test_q_alignment(pa, dev, qt, G):
