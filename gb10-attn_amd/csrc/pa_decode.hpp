@@ -46,6 +46,12 @@
 #ifndef PA_DECODE_PRIO
 #define PA_DECODE_PRIO 0
 #endif
+#ifndef PA_DECODE_LAZY
+#define PA_DECODE_LAZY 1  // raise the softmax reference point only by more than 2^8
+#endif
+#ifndef PA_DECODE_DOT2
+#define PA_DECODE_DOT2 1  // packed dot products for q . k (16-bit caches, q of the cache's dtype)
+#endif
 #ifndef PA_DECODE_MFMA
 #define PA_DECODE_MFMA 1  // GQA groups of >= 4 heads on the matrix-core kernel
 #endif
@@ -87,10 +93,18 @@ constexpr int kBtChunk = 256;  // block-table entries staged in LDS at a time
 // Groups of up to 4 heads are held to two waves per SIMD (<= 256 registers),
 // which the loads in flight need; left to itself the allocator has tipped
 // GC = 4 at D = 128 into one wave per SIMD (config 3: 415 -> 518 us).
-template <typename KV, int D, int GC, int HP = 1>
+// DQ (kF16 or kBF16): q is fp16 or bf16 and the cache provides element pairs
+// of that type (the raw words of a cache of q's dtype; FP8 codes through one
+// packed conversion per pair), so q is held as packed pairs (exact) and each
+// score is VEC / 2 packed dot products (v_dot2c_f32_*), scaled afterwards,
+// instead of widening K to fp32 and VEC fused multiply-adds: the score costs
+// a quarter of the vector instructions (GQA groups are bound by them).
+template <typename KV, int D, int GC, int HP = 1, int DQ = 0>
 __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(GC <= 4 ? 2 : 1)))
 void decode_kernel(const DecodeParams p) {
   static_assert(HP == 1 || GC == 1, "head pairing serves MHA groups");
+  static_assert(DQ == 0 || (pair_types<KV>::value & (1 << DQ)), "the cache cannot provide q's pairs");
+  constexpr bool LAZY = PA_DECODE_LAZY && GC >= 2;
   using Sh = DecodeShape<KV, D * HP>;
   constexpr int VEC = Sh::VEC, LPT = Sh::LPT, TPI = Sh::TPI, NI = Sh::NI, TT = Sh::TT;
   constexpr int LPH = D / VEC;  // lanes per head's row
@@ -171,13 +185,21 @@ void decode_kernel(const DecodeParams p) {
   for (int g = 0; g < GC; ++g) {
     const bool hv = g0 + g < p.G;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) qr[g][e] = hv ? qr[g][e] * p.qscale : 0.0f;
+    for (int e = 0; e < VEC; ++e) qr[g][e] = hv ? (DQ ? qr[g][e] : qr[g][e] * p.qscale) : 0.0f;
+  }
+  uint32_t qp[DQ ? GC : 1][DQ ? VEC / 2 : 1];
+  if constexpr (DQ) {
+#pragma unroll
+    for (int g = 0; g < GC; ++g)
+#pragma unroll
+      for (int w = 0; w < VEC / 2; ++w) qp[g][w] = pack_pair_exact<DQ>(qr[g][2 * w], qr[g][2 * w + 1]);
   }
 
-  float m[GC], l[GC], acc[GC][VEC];
+  float m[GC], l[GC], acc[GC][VEC], mx[GC];
 #pragma unroll
   for (int g = 0; g < GC; ++g) {
     m[g] = kNegBig;
+    mx[g] = kNegBig;
     l[g] = 0.0f;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[g][e] = 0.0f;
@@ -276,38 +298,71 @@ void decode_kernel(const DecodeParams p) {
     float s[NI][GC];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      float kf[VEC];
-      KV::widen(T.k[i], kf);
+      if constexpr (DQ) {
+        uint32_t kp[VEC / 2];
+        KV::template to_pairs<DQ>(T.k[i], kp);
 #pragma unroll
-      for (int g = 0; g < GC; ++g) {
-        float d = 0.0f;
+        for (int g = 0; g < GC; ++g) {
+          float d = 0.0f;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) d = fmaf(qr[g][e], kf[e], d);
-        s[i][g] = group_sum<LPH>(d);
+          for (int w = 0; w < VEC / 2; ++w) d = dot2<DQ>(qp[g][w], kp[w], d);
+          s[i][g] = group_sum<LPH>(d) * p.qscale;
+        }
+      } else {
+        float kf[VEC];
+        KV::widen(T.k[i], kf);
+#pragma unroll
+        for (int g = 0; g < GC; ++g) {
+          float d = 0.0f;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) d = fmaf(qr[g][e], kf[e], d);
+          s[i][g] = group_sum<LPH>(d);
+        }
       }
     }
     float vf[NI][VEC];
 #pragma unroll
     for (int i = 0; i < NI; ++i) KV::widen(T.v[i], vf[i]);
+    // Lazy rescale: a stream's reference point m is raised only when a tile
+    // exceeds it by more than 2^8 (8 in log2 units), so every weight stays
+    // <= 256 (softmax is invariant to the reference point).  The test is
+    // wave-uniform, so the common case skips the correction exponentials and
+    // the accumulator rescale.  mx tracks the true maximum; the streams are
+    // rebased onto it once, after the last tile.  GQA groups only: for one
+    // head per work-group (bound by HBM, not vector work) the branch costs
+    // more than it saves.
+    float mn[GC];
+    uint32_t raise = 0;
 #pragma unroll
     for (int g = 0; g < GC; ++g) {
       float mt = kNegBig;
 #pragma unroll
       for (int i = 0; i < NI; ++i) mt = ((T.live >> i) & 1u) ? fmaxf(mt, s[i][g]) : mt;
-      const float mn = fmaxf(m[g], mt);
-      const float corr = fast_exp2(m[g] - mn);
-      float lg = l[g] * corr;
+      mn[g] = LAZY ? (mt > m[g] + 8.0f ? mt : m[g]) : fmaxf(m[g], mt);
+      raise |= mn[g] != m[g] ? 1u : 0u;
+      if constexpr (LAZY) mx[g] = fmaxf(mx[g], mt);
+    }
+    if (!LAZY || __builtin_amdgcn_ballot_w64(raise != 0) != 0) {
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[g][e] *= corr;
+      for (int g = 0; g < GC; ++g) {
+        const float corr = fast_exp2(m[g] - mn[g]);
+        l[g] *= corr;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[g][e] *= corr;
+        m[g] = mn[g];
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GC; ++g) {
+      float lg = l[g];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        const float pi = ((T.live >> i) & 1u) ? fast_exp2(s[i][g] - mn) : 0.0f;
+        const float pi = ((T.live >> i) & 1u) ? fast_exp2(s[i][g] - m[g]) : 0.0f;
         lg += pi;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc[g][e] = fmaf(pi, vf[i][e], acc[g][e]);
       }
       l[g] = lg;
-      m[g] = mn;
     }
   };
 
@@ -365,6 +420,19 @@ void decode_kernel(const DecodeParams p) {
       } else {
         sweep(issue);
       }
+    }
+  }
+
+  // Rebase each stream from its lazy reference point onto its true maximum
+  // (the partials carry the maximum, kernels/paged_attn_v3.cu:113-122).
+  if constexpr (LAZY) {
+#pragma unroll
+    for (int g = 0; g < GC; ++g) {
+      const float corr = fast_exp2(m[g] - mx[g]);
+      l[g] *= corr;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[g][e] *= corr;
+      m[g] = mx[g];
     }
   }
 
@@ -436,6 +504,21 @@ void decode_kernel(const DecodeParams p) {
 template <typename KV, int D, int GC, int HP = 1>
 hipError_t launch_decode_dg(const DecodeParams& p, hipStream_t stream) {
   const int64_t blocks = (int64_t)p.B * p.Sq * (p.HKV / HP) * p.head_chunks * p.parts;
+  constexpr int PTS = PA_DECODE_DOT2 ? pair_types<KV>::value : 0;
+  if constexpr ((PTS >> kF16) & 1) {
+    if (p.q_dtype == kF16) {
+      hipLaunchKernelGGL((decode_kernel<KV, D, GC, HP, kF16>), dim3((unsigned)blocks), dim3(kDecodeThreads), 0,
+                         stream, p);
+      return hipGetLastError();
+    }
+  }
+  if constexpr ((PTS >> kBF16) & 1) {
+    if (p.q_dtype == kBF16) {
+      hipLaunchKernelGGL((decode_kernel<KV, D, GC, HP, kBF16>), dim3((unsigned)blocks), dim3(kDecodeThreads), 0,
+                         stream, p);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL((decode_kernel<KV, D, GC, HP>), dim3((unsigned)blocks), dim3(kDecodeThreads), 0,
                      stream, p);
   return hipGetLastError();

@@ -13,6 +13,8 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------- KV types --
 // Each KV storage type is read 16 bytes per lane (one global_load_dwordx4;
@@ -28,6 +30,13 @@ struct KvF16 {
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = (float)h[e];
   }
+  // Element pairs for packed dot products: the raw words already are.
+  static constexpr int kPairs = 1 << kF16;
+  template <int PT>
+  __device__ static inline void to_pairs(const u32x4_t& r, uint32_t (&o)[kVec / 2]) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w] = r[w];
+  }
 };
 
 struct KvBF16 {
@@ -41,6 +50,12 @@ struct KvBF16 {
       o[2 * w] = __builtin_bit_cast(float, r[w] << 16);
       o[2 * w + 1] = __builtin_bit_cast(float, r[w] & 0xffff0000u);
     }
+  }
+  static constexpr int kPairs = 1 << kBF16;
+  template <int PT>
+  __device__ static inline void to_pairs(const u32x4_t& r, uint32_t (&o)[kVec / 2]) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w] = r[w];
   }
 };
 
@@ -97,7 +112,48 @@ struct KvFP8 {
       o[4 * w + 3] = hi[1];
     }
   }
+  // Element pairs in fp16 or bf16 (v_cvt_scalef32_pk_{f16,bf16}_fp8 with
+  // scale 1: exact for every code, NaN included).
+  static constexpr int kPairs = (1 << kF16) | (1 << kBF16);
+  template <int PT>
+  __device__ static inline void to_pairs(const Raw& r, uint32_t (&o)[kVec / 2]) {
+#pragma unroll
+    for (int w = 0; w < kVec / 4; ++w) {
+      if constexpr (PT == kF16) {
+        o[2 * w] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(r[w], 1.0f, false));
+        o[2 * w + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(r[w], 1.0f, true));
+      } else {
+        o[2 * w] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r[w], 1.0f, false));
+        o[2 * w + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r[w], 1.0f, true));
+      }
+    }
+  }
 };
+
+// Packed dot products over 16-bit element pairs (PT = kF16 or kBF16):
+// c + a.lo * b.lo + a.hi * b.hi (v_dot2c_f32_f16 / v_dot2c_f32_bf16), and the
+// pair of two fp32 values that PT represents exactly (element 0 low).
+template <int PT>
+__device__ inline float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (PT == kF16)
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+                                          false);
+}
+template <int PT>
+__device__ inline uint32_t pack_pair_exact(float x, float y) {
+  if constexpr (PT == kF16)
+    return __builtin_bit_cast(uint32_t, f16x2_t{(_Float16)x, (_Float16)y});
+  else
+    return (__builtin_bit_cast(uint32_t, x) >> 16) | (__builtin_bit_cast(uint32_t, y) & 0xffff0000u);
+}
+
+// Which 16-bit pair types a cache type provides (0: none).
+template <typename KV, typename = void>
+struct pair_types { static constexpr int value = 0; };
+template <typename KV>
+struct pair_types<KV, std::void_t<decltype(KV::kPairs)>> { static constexpr int value = KV::kPairs; };
 
 template <int NT = 0>
 __device__ inline u32x4_t load16(const void* base, int64_t byte_off) {
