@@ -115,6 +115,12 @@ __device__ inline void load8f(const void* q, int dtype, int64_t idx, float (&x)[
   }
 }
 
+#ifndef PA_PF_STORE
+#define PA_PF_STORE 1  // output stores: 0 per element, 1 vector, 2 vector non-temporal, 3 vector device-scope
+#endif
+#ifndef PA_PF_KB64
+#define PA_PF_KB64 64  // keys per tile at D <= 64
+#endif
 constexpr int kPfThreads = 256;   // 4 waves
 constexpr int kPfBtStage = 1024;  // block-table entries staged in LDS
 constexpr float kLazyRescale = 8.0f;  // raise the running max only past 2^8
@@ -135,7 +141,7 @@ template <int D>
 struct PfShape {
   static constexpr int QW = 32;                  // query rows per wave (one MFMA n-tile)
   static constexpr int QB = 4 * QW;              // query rows per work-group
-  static constexpr int KB = D <= 128 ? 64 : 32;  // keys per tile
+  static constexpr int KB = D <= 64 ? PA_PF_KB64 : D <= 128 ? 64 : 32;  // keys per tile
   static constexpr int MT = KB / 32;             // 32-key m-tiles of S^T
   static constexpr int KS = D / 16;              // 16-dim k-steps of Q.K^T
   static constexpr int DT = D / 32;              // 32-dim m-tiles of O^T
@@ -341,15 +347,16 @@ void prefill_mfma_kernel(const PrefillParams p) {
   }
   int badkey = 0x7fffffff;
 
-  // Row offsets of a tile, built once per tile by wave 0 (one row per lane)
-  // two tiles ahead, so the other waves' loads cost one LDS read and an add
+  // Row offsets of a tile, built once per tile by the first KB / 64 waves (one
+  // row per lane) two tiles ahead, so the other waves' loads cost one LDS read and an add
   // per chunk.  Entry r = {K byte offset, V byte offset | use}; a row past
   // kend, or on a page with an invalid block id, points at row 0 of block 0
   // (in bounds, NB >= 1) with use = 0.  Offsets are multiples of 16 bytes, so
   // bit 0 of the V offset is free for the flag.
   auto build = [&](int t, u64x2_t* tb) {
-    if (wave == 0 && lane < KB) {
-      const int kabs = t * KB + lane;
+    if (wave * 64 + lane < KB) {
+      const int row = wave * 64 + lane;
+      const int kabs = t * KB + row;
       const bool valid = kabs < kend;
       const int kk = valid ? kabs : 0;
       const int pg = (int)fastdiv((uint32_t)kk, p.bs_div);
@@ -359,8 +366,8 @@ void prefill_mfma_kernel(const PrefillParams p) {
       if (valid && !okb) badkey = min(badkey, kabs);
       const bool use = valid && okb;
       const uint32_t ub = use ? (uint32_t)blk : 0u, uo = use ? (uint32_t)off : 0u;
-      tb[lane] = u64x2_t{(uint64_t)ub * k_sbb + uo * k_stb,
-                         ((uint64_t)ub * v_sbb + uo * v_stb) | (use ? 1u : 0u)};
+      tb[row] = u64x2_t{(uint64_t)ub * k_sbb + uo * k_stb,
+                        ((uint64_t)ub * v_sbb + uo * v_stb) | (use ? 1u : 0u)};
     }
   };
 
@@ -625,12 +632,54 @@ void prefill_mfma_kernel(const PrefillParams p) {
   const bool bad = bad_from <= qpos;
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
   const int64_t orow = ((tok0 + qrow) * p.H + h) * D;
+  // Slots 4j .. 4j+3 of m-tile dt are 4 consecutive dims: one 8-byte (16-bit
+  // out) or 16-byte (fp32 out) store when the output base allows it.
+  const uintptr_t oa = reinterpret_cast<uintptr_t>(p.out);
+  const bool vec = PA_PF_STORE != 0 && (p.out_dtype == kF32 ? (oa & 15) == 0 : (oa & 7) == 0);
+  if (!vec) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = dt * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+        store_elem(p.out, p.out_dtype, orow + d, bad ? __builtin_nanf("") : o[dt][r] * inv);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int d = dt * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-      store_elem(p.out, p.out_dtype, orow + d, bad ? __builtin_nanf("") : o[dt][r] * inv);
+    for (int j = 0; j < 4; ++j) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = bad ? __builtin_nanf("") : o[dt][4 * j + i] * inv;
+      const int64_t e = orow + dt * 32 + 8 * j + 4 * hh;
+      if (p.out_dtype == kF32) {
+        u64x2_t w = u64x2_t{(uint64_t)__builtin_bit_cast(uint32_t, v[0]) | ((uint64_t)__builtin_bit_cast(uint32_t, v[1]) << 32),
+                            (uint64_t)__builtin_bit_cast(uint32_t, v[2]) | ((uint64_t)__builtin_bit_cast(uint32_t, v[3]) << 32)};
+        u64x2_t* dst = reinterpret_cast<u64x2_t*>(static_cast<float*>(p.out) + e);
+        if constexpr (PA_PF_STORE == 2) {
+          __builtin_nontemporal_store(w, dst);
+        } else if constexpr (PA_PF_STORE == 3) {
+          __hip_atomic_store(reinterpret_cast<uint64_t*>(dst), w[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(reinterpret_cast<uint64_t*>(dst) + 1, w[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          *dst = w;
+        }
+      } else {
+        const uint32_t w0 = p.out_dtype == kF16 ? pack2<false>(v[0], v[1]) : pack2<true>(v[0], v[1]);
+        const uint32_t w1 = p.out_dtype == kF16 ? pack2<false>(v[2], v[3]) : pack2<true>(v[2], v[3]);
+        const uint64_t w = (uint64_t)w0 | ((uint64_t)w1 << 32);
+        uint64_t* dst = reinterpret_cast<uint64_t*>(static_cast<uint16_t*>(p.out) + e);
+        if constexpr (PA_PF_STORE == 2) {
+          __builtin_nontemporal_store(w, dst);
+        } else if constexpr (PA_PF_STORE == 3) {
+          __hip_atomic_store(dst, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          *dst = w;
+        }
+      }
     }
   }
 }

@@ -70,6 +70,22 @@ def test_mfma_prefill_dtypes(pa, dev, qt, ot):
     close(to_host(got), want_of(inp, 0.125))
 
 
+@pytest.mark.parametrize("ot", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shift", [0, 1, 2, 4])
+def test_mfma_prefill_output_alignment(pa, dev, ot, shift):
+    """The epilogue writes 4 consecutive dims per store (8 bytes for 16-bit
+    out, 16 for fp32) when the output base allows it and single elements
+    otherwise: outputs at element offsets 0, 1, 2 and 4 into a larger buffer
+    cover both paths for every output dtype, D = 64 and 128."""
+    for D in (64, 128):
+        inp = prefill_case(2, 70, 4, 2, D, 16, [70, 130], seed=31 + shift + D, kv="f16", qt="f16")
+        q = to_dev(inp["q"], "f16", dev)
+        buf = torch.full((q.numel() + shift,), float("nan"), dtype=ot, device=dev)
+        out = buf[shift:].view(q.shape)
+        pa.paged_attention_prefill_wmma(q, *dev_args(inp, dev)[1:], 0.1, out=out)
+        close(to_host(out), want_of(inp, 0.1))
+
+
 def test_mfma_prefill_config4a_shape(pa, dev):
     """BASELINE config 4a geometry (H=12, D=64, fp16, BS=16, S=ctx=1024), batch 2."""
     inp = prefill_case(2, 1024, 12, 12, 64, 16, [1024, 1024], seed=44, kv="f16", qt="f16")
