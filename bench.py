@@ -732,7 +732,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": traffic_from_profiles("decode_c2"),
-                     "kernel": "pa::decode_kernel<KvF16, 64, 1>",
+                     "kernel": "pa::decode_kernel<KvF16, 64, 1, 1, 1>",
                      "kernel_ms": round(kms, 5), "bytes_per_launch": int(work.bytes)},
     }
     log("bench: cpu baseline (reference cpu_reference, 1 thread)")
