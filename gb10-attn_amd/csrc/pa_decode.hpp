@@ -34,6 +34,9 @@
 #ifndef PA_DECODE_NI
 #define PA_DECODE_NI 4
 #endif
+#ifndef PA_DECODE_NI_MHA
+#define PA_DECODE_NI_MHA 2  // loads per lane per tile for one unpacked MHA head per work-group (config 2: +0.8 % over 4)
+#endif
 #ifndef PA_DECODE_PIPE
 #define PA_DECODE_PIPE 1
 #endif
@@ -69,13 +72,13 @@ constexpr int kni() {
   return PA_DECODE_NI;
 }
 
-template <typename KV, int D>
+template <typename KV, int D, int NIO = 0>
 struct DecodeShape {
   static constexpr int VEC = KV::kVec;         // elements per lane per load
   static constexpr int LPT = D / VEC;          // lanes per token row
   static_assert(LPT >= 1 && LPT <= 64 && (LPT & (LPT - 1)) == 0, "unsupported D/KV combination");
   static constexpr int TPI = 64 / LPT;         // token rows per load instruction
-  static constexpr int NI = kni<KV>();         // K (and V) loads per lane per tile
+  static constexpr int NI = NIO > 0 ? NIO : kni<KV>();  // K (and V) loads per lane per tile
   static constexpr int TT = NI * TPI;          // tokens per wave tile
 };
 
@@ -105,7 +108,7 @@ void decode_kernel(const DecodeParams p) {
   static_assert(HP == 1 || GC == 1, "head pairing serves MHA groups");
   static_assert(DQ == 0 || (pair_types<KV>::value & (1 << DQ)), "the cache cannot provide q's pairs");
   constexpr bool LAZY = PA_DECODE_LAZY && GC >= 2;
-  using Sh = DecodeShape<KV, D * HP>;
+  using Sh = DecodeShape<KV, D * HP, (GC == 1 && HP == 1) ? PA_DECODE_NI_MHA : 0>;
   constexpr int VEC = Sh::VEC, LPT = Sh::LPT, TPI = Sh::TPI, NI = Sh::NI, TT = Sh::TT;
   constexpr int LPH = D / VEC;  // lanes per head's row
   constexpr int NW = kDecodeWaves;
