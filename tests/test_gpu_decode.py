@@ -482,6 +482,33 @@ def test_head_packing_wide_rows(pa, dev, kind, D, HKV, BS):
         close(got2, want2)
 
 
+@pytest.mark.parametrize("kv", ["f16", "bf16", "fp8"])
+@pytest.mark.parametrize("H,HKV", [(2, 2), (8, 2)])
+def test_long_sequence_many_partitions(pa, dev, kv, H, HKV):
+    """One 32768-token sequence: the auto plan has too few (sequence, head)
+    units to fill the GPU and cuts the context into 128 partitions of 256
+    tokens (more than one 64-lane window of the reduce kernel, fixed-length
+    mode), with two heads packed per work-group for MHA and the lazy softmax
+    rescale for the GQA group; a second sequence of 300 tokens rides along."""
+    ctx = [32768, 300]
+    D = 64
+    if kv == "fp8":
+        inp, k8, v8, kf, vf = fp8_case(len(ctx), H, HKV, D, 16, ctx, seed=40 + H, k_scale=1.0, v_scale=1.0)
+        q = torch.from_numpy(inp["q_f32"]).to(dev).half()
+        k, v = fp8_dev(k8, dev), fp8_dev(v8, dev)
+        want = oracle.decode(oracle.to_float(oracle.quantize(inp["q_f32"], "f16"), "f16"), kf, vf, inp["bt"],
+                             inp["ctx"], 0.125, "f32")
+    else:
+        inp = decode_case(len(ctx), H, HKV, D, 16, ctx, seed=40 + H, kv=kv, q=kv)
+        q, k, v, _, _ = dev_inputs(inp, dev)
+        want = want_of(inp, 0.125)
+    bt, ctxd = torch.from_numpy(inp["bt"]).to(dev), torch.from_numpy(inp["ctx"]).to(dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    ptok, nparts = pa.plan_partitions(len(ctx), H, HKV, D, 32768, cus)
+    assert nparts > 64 and ptok * nparts >= 32768
+    close(to_host(pa.paged_attention_v3(q, k, v, bt, ctxd, 0.125, 0)), want)
+
+
 @pytest.mark.parametrize("qt", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("G", [1, 4, 8])
 def test_q_alignment(pa, dev, qt, G):
