@@ -52,6 +52,9 @@
 #ifndef PA_DECODE_LAZY
 #define PA_DECODE_LAZY 1  // raise the softmax reference point only by more than 2^8
 #endif
+#ifndef PA_DECODE_PVDOT
+#define PA_DECODE_PVDOT 1  // GQA groups over fp16/FP8 caches: P.V as packed fp16 dot products over token pairs
+#endif
 #ifndef PA_DECODE_DOT2
 #define PA_DECODE_DOT2 1  // packed dot products for q . k (16-bit caches, q of the cache's dtype)
 #endif
@@ -110,6 +113,10 @@ void decode_kernel(const DecodeParams p) {
   constexpr bool LAZY = PA_DECODE_LAZY && GC >= 2;
   using Sh = DecodeShape<KV, D * HP, (GC == 1 && HP == 1) ? PA_DECODE_NI_MHA : 0>;
   constexpr int VEC = Sh::VEC, LPT = Sh::LPT, TPI = Sh::TPI, NI = Sh::NI, TT = Sh::TT;
+  // Packed P.V for GQA groups over fp16 or FP8 caches (V as fp16 pairs);
+  // bf16 weights would be too coarse, so bf16 caches keep the fp32 path.
+  constexpr bool PVP = PA_DECODE_PVDOT && LAZY && (Sh::NI % 2 == 0) && KV::kCode != kBF16 &&
+                       ((pair_types<KV>::value >> kF16) & 1);
   constexpr int LPH = D / VEC;  // lanes per head's row
   constexpr int NW = kDecodeWaves;
 
@@ -323,9 +330,25 @@ void decode_kernel(const DecodeParams p) {
         }
       }
     }
-    float vf[NI][VEC];
+    // V for P.V: fp32 rows (vf), or, on the packed path, element pairs across
+    // two tokens (vlo: element 2w of tokens 2u and 2u+1, vhi: element 2w+1).
+    float vf[PVP ? 1 : NI][PVP ? 1 : VEC];
+    uint32_t vlo[PVP ? NI / 2 : 1][PVP ? VEC / 2 : 1], vhi[PVP ? NI / 2 : 1][PVP ? VEC / 2 : 1];
+    if constexpr (PVP) {
+      uint32_t vp[NI][VEC / 2];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) KV::widen(T.v[i], vf[i]);
+      for (int i = 0; i < NI; ++i) KV::template to_pairs<kF16>(T.v[i], vp[i]);
+#pragma unroll
+      for (int u = 0; u < NI / 2; ++u)
+#pragma unroll
+        for (int w = 0; w < VEC / 2; ++w) {
+          vlo[u][w] = __builtin_amdgcn_perm(vp[2 * u + 1][w], vp[2 * u][w], 0x05040100u);
+          vhi[u][w] = __builtin_amdgcn_perm(vp[2 * u + 1][w], vp[2 * u][w], 0x07060302u);
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) KV::widen(T.v[i], vf[i]);
+    }
     // Lazy rescale: a stream's reference point m is raised only when a tile
     // exceeds it by more than 2^8 (8 in log2 units), so every weight stays
     // <= 256 (softmax is invariant to the reference point).  The test is
@@ -358,12 +381,30 @@ void decode_kernel(const DecodeParams p) {
 #pragma unroll
     for (int g = 0; g < GC; ++g) {
       float lg = l[g];
+      if constexpr (PVP) {
+        // Weights of two tokens as one fp16 pair (<= 256 by the lazy rescale;
+        // 2^-12 relative rounding), the row sum over the same rounded weights,
+        // then one packed dot product per element: acc[e] += p0 v0[e] + p1 v1[e].
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        const float pi = ((T.live >> i) & 1u) ? fast_exp2(s[i][g] - m[g]) : 0.0f;
-        lg += pi;
+        for (int u = 0; u < NI / 2; ++u) {
+          const float p0 = ((T.live >> (2 * u)) & 1u) ? fast_exp2(s[2 * u][g] - m[g]) : 0.0f;
+          const float p1 = ((T.live >> (2 * u + 1)) & 1u) ? fast_exp2(s[2 * u + 1][g] - m[g]) : 0.0f;
+          const uint32_t pp = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{p0, p1}, f16x2_t));
+          lg = dot2<kF16>(pp, 0x3c003c00u, lg);
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) acc[g][e] = fmaf(pi, vf[i][e], acc[g][e]);
+          for (int w = 0; w < VEC / 2; ++w) {
+            acc[g][2 * w] = dot2<kF16>(vlo[u][w], pp, acc[g][2 * w]);
+            acc[g][2 * w + 1] = dot2<kF16>(vhi[u][w], pp, acc[g][2 * w + 1]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const float pi = ((T.live >> i) & 1u) ? fast_exp2(s[i][g] - m[g]) : 0.0f;
+          lg += pi;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[g][e] = fmaf(pi, vf[i][e], acc[g][e]);
+        }
       }
       l[g] = lg;
     }
