@@ -116,7 +116,7 @@ __device__ inline void load8f(const void* q, int dtype, int64_t idx, float (&x)[
 }
 
 #ifndef PA_PF_STORE
-#define PA_PF_STORE 1  // output stores: 0 per element, 1 vector, 2 vector non-temporal, 3 vector device-scope
+#define PA_PF_STORE 1  // output stores: 1 four dims per store where the base allows it, 0 per element
 #endif
 #ifndef PA_PF_KB64
 #define PA_PF_KB64 64  // keys per tile at D <= 64
@@ -658,27 +658,12 @@ void prefill_mfma_kernel(const PrefillParams p) {
       if (p.out_dtype == kF32) {
         u64x2_t w = u64x2_t{(uint64_t)__builtin_bit_cast(uint32_t, v[0]) | ((uint64_t)__builtin_bit_cast(uint32_t, v[1]) << 32),
                             (uint64_t)__builtin_bit_cast(uint32_t, v[2]) | ((uint64_t)__builtin_bit_cast(uint32_t, v[3]) << 32)};
-        u64x2_t* dst = reinterpret_cast<u64x2_t*>(static_cast<float*>(p.out) + e);
-        if constexpr (PA_PF_STORE == 2) {
-          __builtin_nontemporal_store(w, dst);
-        } else if constexpr (PA_PF_STORE == 3) {
-          __hip_atomic_store(reinterpret_cast<uint64_t*>(dst), w[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(reinterpret_cast<uint64_t*>(dst) + 1, w[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-          *dst = w;
-        }
+        *reinterpret_cast<u64x2_t*>(static_cast<float*>(p.out) + e) = w;
       } else {
         const uint32_t w0 = p.out_dtype == kF16 ? pack2<false>(v[0], v[1]) : pack2<true>(v[0], v[1]);
         const uint32_t w1 = p.out_dtype == kF16 ? pack2<false>(v[2], v[3]) : pack2<true>(v[2], v[3]);
         const uint64_t w = (uint64_t)w0 | ((uint64_t)w1 << 32);
-        uint64_t* dst = reinterpret_cast<uint64_t*>(static_cast<uint16_t*>(p.out) + e);
-        if constexpr (PA_PF_STORE == 2) {
-          __builtin_nontemporal_store(w, dst);
-        } else if constexpr (PA_PF_STORE == 3) {
-          __hip_atomic_store(dst, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-          *dst = w;
-        }
+        *reinterpret_cast<uint64_t*>(static_cast<uint16_t*>(p.out) + e) = w;
       }
     }
   }
