@@ -151,7 +151,11 @@ int64_t choose_num_splits_for(int64_t num_seqs, int64_t num_heads, int64_t max_c
 
 /* The partition plan paged_attention_v3 uses when num_splits <= 0, for an
  * explicit CU count; pure, needs no GPU.  Writes the partition length in
- * tokens and the number of partitions per sequence (1 = no split). */
+ * tokens and the number of partitions per sequence (1 = no split).  It
+ * sees no cache layout: for MHA caches whose head rows are shorter than 128
+ * bytes (served two heads per work-group) paged_attention_v3 plans with
+ * num_kv_heads / 2 units; paged_attention_v3_workspace_size always matches
+ * the call. */
 int pa_plan_partitions(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads,
                        int64_t head_dim, int64_t max_context, int64_t num_compute_units,
                        int64_t* partition_tokens, int64_t* num_partitions);
