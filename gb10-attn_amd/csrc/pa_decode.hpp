@@ -55,6 +55,9 @@
 #ifndef PA_DECODE_ROT
 #define PA_DECODE_ROT 1  // rotate the head order per (sequence, partition) for one-head work-groups
 #endif
+#ifndef PA_DECODE_PBCAST
+#define PA_DECODE_PBCAST 1  // groups of four heads: one exponential per lane, shared across the quad
+#endif
 #ifndef PA_DECODE_PVDOT
 #define PA_DECODE_PVDOT 1  // GQA groups over fp16/FP8 caches: P.V as packed fp16 dot products over token pairs
 #endif
@@ -118,6 +121,10 @@ void decode_kernel(const DecodeParams p) {
   constexpr int VEC = Sh::VEC, LPT = Sh::LPT, TPI = Sh::TPI, NI = Sh::NI, TT = Sh::TT;
   // Packed P.V for GQA groups over fp16 or FP8 caches (V as fp16 pairs);
   // bf16 weights would be too coarse, so bf16 caches keep the fp32 path.
+  // Groups of four heads whose token row spans one 16-lane DPP row: each lane
+  // of a quad finishes one head's score (transposing reduction) and its
+  // exponential, shared across the quad.
+  constexpr bool PBC = PA_DECODE_PBCAST && LAZY && GC == 4 && LPT == 16;
   constexpr bool PVP = PA_DECODE_PVDOT && LAZY && (Sh::NI % 2 == 0) && KV::kCode != kBF16 &&
                        ((pair_types<KV>::value >> kF16) & 1);
   constexpr int LPH = D / VEC;  // lanes per head's row
@@ -216,6 +223,7 @@ void decode_kernel(const DecodeParams p) {
   }
 
   float m[GC], l[GC], acc[GC][VEC], mx[GC];
+  float m_own = kNegBig, mx_own = kNegBig;  // PBC: this lane's head's reference point and true maximum
 #pragma unroll
   for (int g = 0; g < GC; ++g) {
     m[g] = kNegBig;
@@ -315,29 +323,49 @@ void decode_kernel(const DecodeParams p) {
 
   // Online-softmax update of this lane group's streams with one tile.
   auto consume = [&](const Tile& T) {
-    float s[NI][GC];
+    float s[PBC ? 1 : NI][PBC ? 1 : GC];  // every head's score of each token
+    float so[PBC ? NI : 1];                // PBC: this lane's head's score
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
+      float d[GC];  // this lane's partial dot products
       if constexpr (DQ) {
         uint32_t kp[VEC / 2];
         KV::template to_pairs<DQ>(T.k[i], kp);
 #pragma unroll
         for (int g = 0; g < GC; ++g) {
-          float d = 0.0f;
+          d[g] = 0.0f;
 #pragma unroll
-          for (int w = 0; w < VEC / 2; ++w) d = dot2<DQ>(qp[g][w], kp[w], d);
-          s[i][g] = group_sum<LPH>(d) * p.qscale;
+          for (int w = 0; w < VEC / 2; ++w) d[g] = dot2<DQ>(qp[g][w], kp[w], d[g]);
         }
       } else {
         float kf[VEC];
         KV::widen(T.k[i], kf);
 #pragma unroll
         for (int g = 0; g < GC; ++g) {
-          float d = 0.0f;
+          d[g] = 0.0f;
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) d = fmaf(qr[g][e], kf[e], d);
-          s[i][g] = group_sum<LPH>(d);
+          for (int e = 0; e < VEC; ++e) d[g] = fmaf(qr[g][e], kf[e], d[g]);
         }
+      }
+      const float sc = DQ ? p.qscale : 1.0f;
+      if constexpr (PBC) {
+        // Transposing sum over the 16-lane slot: after the two quad steps
+        // lane j of each quad holds head j's sum over the quad, then the
+        // four quads are added (row rotations by 4 and 8).
+        const bool b0 = (lane & 1) != 0, b1 = (lane & 2) != 0;
+        float k0 = b0 ? d[1] : d[0], k1 = b0 ? d[3] : d[2];
+        const float t0 = b0 ? d[0] : d[1], t1 = b0 ? d[2] : d[3];
+        k0 += dpp<kDppXor1>(t0);
+        k1 += dpp<kDppXor1>(t1);
+        float k = b1 ? k1 : k0;
+        const float t = b1 ? k0 : k1;
+        k += dpp<kDppXor2>(t);
+        k += dpp<kDppRor4>(k);
+        k += dpp<kDppRor8>(k);
+        so[i] = k * sc;
+      } else {
+#pragma unroll
+        for (int g = 0; g < GC; ++g) s[i][g] = group_sum<LPH>(d[g]) * sc;
       }
     }
     // V for P.V: fp32 rows (vf), or, on the packed path, element pairs across
@@ -359,34 +387,70 @@ void decode_kernel(const DecodeParams p) {
 #pragma unroll
       for (int i = 0; i < NI; ++i) KV::widen(T.v[i], vf[i]);
     }
-    // Lazy rescale: a stream's reference point m is raised only when a tile
-    // exceeds it by more than 2^8 (8 in log2 units), so every weight stays
-    // <= 256 (softmax is invariant to the reference point).  The test is
-    // wave-uniform, so the common case skips the correction exponentials and
-    // the accumulator rescale.  mx tracks the true maximum; the streams are
-    // rebased onto it once, after the last tile.  GQA groups only: for one
-    // head per work-group (bound by HBM, not vector work) the branch costs
-    // more than it saves.
-    float mn[GC];
-    uint32_t raise = 0;
-#pragma unroll
-    for (int g = 0; g < GC; ++g) {
+    float pw[NI][GC];  // weights 2^(s - m) of each token and head
+    if constexpr (PBC) {
+      // The lane's own head: its tile maximum, the lazy test against its
+      // reference point, and one exponential per token, shared across the quad.
       float mt = kNegBig;
 #pragma unroll
-      for (int i = 0; i < NI; ++i) mt = ((T.live >> i) & 1u) ? fmaxf(mt, s[i][g]) : mt;
-      mn[g] = LAZY ? (mt > m[g] + 8.0f ? mt : m[g]) : fmaxf(m[g], mt);
-      raise |= mn[g] != m[g] ? 1u : 0u;
-      if constexpr (LAZY) mx[g] = fmaxf(mx[g], mt);
-    }
-    if (!LAZY || __builtin_amdgcn_ballot_w64(raise != 0) != 0) {
+      for (int i = 0; i < NI; ++i) mt = ((T.live >> i) & 1u) ? fmaxf(mt, so[i]) : mt;
+      mx_own = fmaxf(mx_own, mt);
+      const bool up = mt > m_own + 8.0f;
+      if (__builtin_amdgcn_ballot_w64(up) != 0) {
+        const float mtg[4] = {dpp<0x00>(mt), dpp<0x55>(mt), dpp<0xAA>(mt), dpp<0xFF>(mt)};
+#pragma unroll
+        for (int g = 0; g < GC; ++g) {
+          const float mn = mtg[g] > m[g] + 8.0f ? mtg[g] : m[g];
+          const float corr = fast_exp2(m[g] - mn);
+          l[g] *= corr;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[g][e] *= corr;
+          m[g] = mn;
+        }
+        m_own = up ? mt : m_own;
+      }
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const float pl = ((T.live >> i) & 1u) ? fast_exp2(so[i] - m_own) : 0.0f;
+        pw[i][0] = dpp<0x00>(pl);
+        pw[i][1] = dpp<0x55>(pl);
+        pw[i][2] = dpp<0xAA>(pl);
+        pw[i][3] = dpp<0xFF>(pl);
+      }
+    } else {
+      // Lazy rescale: a stream's reference point m is raised only when a tile
+      // exceeds it by more than 2^8 (8 in log2 units), so every weight stays
+      // <= 256 (softmax is invariant to the reference point).  The test is
+      // wave-uniform, so the common case skips the correction exponentials and
+      // the accumulator rescale.  mx tracks the true maximum; the streams are
+      // rebased onto it once, after the last tile.  GQA groups only: for one
+      // head per work-group (bound by HBM, not vector work) the branch costs
+      // more than it saves.
+      float mn[GC];
+      uint32_t raise = 0;
 #pragma unroll
       for (int g = 0; g < GC; ++g) {
-        const float corr = fast_exp2(m[g] - mn[g]);
-        l[g] *= corr;
+        float mt = kNegBig;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) acc[g][e] *= corr;
-        m[g] = mn[g];
+        for (int i = 0; i < NI; ++i) mt = ((T.live >> i) & 1u) ? fmaxf(mt, s[i][g]) : mt;
+        mn[g] = LAZY ? (mt > m[g] + 8.0f ? mt : m[g]) : fmaxf(m[g], mt);
+        raise |= mn[g] != m[g] ? 1u : 0u;
+        if constexpr (LAZY) mx[g] = fmaxf(mx[g], mt);
       }
+      if (!LAZY || __builtin_amdgcn_ballot_w64(raise != 0) != 0) {
+#pragma unroll
+        for (int g = 0; g < GC; ++g) {
+          const float corr = fast_exp2(m[g] - mn[g]);
+          l[g] *= corr;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[g][e] *= corr;
+          m[g] = mn[g];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int g = 0; g < GC; ++g) pw[i][g] = ((T.live >> i) & 1u) ? fast_exp2(s[i][g] - m[g]) : 0.0f;
     }
 #pragma unroll
     for (int g = 0; g < GC; ++g) {
@@ -397,8 +461,8 @@ void decode_kernel(const DecodeParams p) {
         // then one packed dot product per element: acc[e] += p0 v0[e] + p1 v1[e].
 #pragma unroll
         for (int u = 0; u < NI / 2; ++u) {
-          const float p0 = ((T.live >> (2 * u)) & 1u) ? fast_exp2(s[2 * u][g] - m[g]) : 0.0f;
-          const float p1 = ((T.live >> (2 * u + 1)) & 1u) ? fast_exp2(s[2 * u + 1][g] - m[g]) : 0.0f;
+          const float p0 = pw[2 * u][g];
+          const float p1 = pw[2 * u + 1][g];
           const uint32_t pp = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{p0, p1}, f16x2_t));
           lg = dot2<kF16>(pp, 0x3c003c00u, lg);
 #pragma unroll
@@ -410,7 +474,7 @@ void decode_kernel(const DecodeParams p) {
       } else {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-          const float pi = ((T.live >> i) & 1u) ? fast_exp2(s[i][g] - m[g]) : 0.0f;
+          const float pi = pw[i][g];
           lg += pi;
 #pragma unroll
           for (int e = 0; e < VEC; ++e) acc[g][e] = fmaf(pi, vf[i][e], acc[g][e]);
@@ -480,6 +544,12 @@ void decode_kernel(const DecodeParams p) {
   // Rebase each stream from its lazy reference point onto its true maximum
   // (the partials carry the maximum, kernels/paged_attn_v3.cu:113-122).
   if constexpr (LAZY) {
+    if constexpr (PBC) {  // the heads' maxima live in the quad's lanes
+      mx[0] = dpp<0x00>(mx_own);
+      mx[1] = dpp<0x55>(mx_own);
+      mx[2] = dpp<0xAA>(mx_own);
+      mx[3] = dpp<0xFF>(mx_own);
+    }
 #pragma unroll
     for (int g = 0; g < GC; ++g) {
       const float corr = fast_exp2(m[g] - mx[g]);

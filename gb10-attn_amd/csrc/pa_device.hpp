@@ -294,6 +294,8 @@ constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i inside each 8-lane half row
 constexpr int kDppMirror = 0x140;     // lane i <-> 15-i inside each 16-lane row
+constexpr int kDppRor4 = 0x124;       // lane i reads lane (i - 4) mod 16 of its 16-lane row
+constexpr int kDppRor8 = 0x128;       // lane i reads lane (i - 8) mod 16 of its 16-lane row
 
 // Sum over aligned groups of N consecutive lanes (N a power of two <= 64);
 // every lane of a group receives the group's total.
