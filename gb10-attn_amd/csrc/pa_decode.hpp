@@ -360,12 +360,31 @@ void decode_kernel(const DecodeParams p) {
         float k = b1 ? k1 : k0;
         const float t = b1 ? k0 : k1;
         k += dpp<kDppXor2>(t);
-        k += dpp<kDppRor4>(k);
+        // Rotation by 8 first: quad q then holds (P_q + P_q+2) + (P_q+1 + P_q+3)
+        // in an order that differs between quads only by commuting operands,
+        // so all four quads hold bitwise-identical sums.
         k += dpp<kDppRor8>(k);
+        k += dpp<kDppRor4>(k);
         so[i] = k * sc;
       } else {
 #pragma unroll
         for (int g = 0; g < GC; ++g) s[i][g] = group_sum<LPH>(d[g]) * sc;
+      }
+    }
+    // A masked token has weight 0, but its V row may be the rest of the last
+    // page past the context end, or row `slot` of block 0 substituted for a
+    // token past the partition, and either may hold any bits: 0 * NaN is NaN.
+    // On tiles with a masked token (a wave-uniform test, so full tiles pay
+    // one ballot) those rows are zeroed before P.V; all-zero bits are +0 in
+    // every KV type.
+    typename KV::Raw vr[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) vr[i] = T.v[i];
+    if (__builtin_amdgcn_ballot_w64(T.live != (1u << NI) - 1u) != 0) {
+      asm volatile("");  // keep this a branch: full tiles skip the selects
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        if (!((T.live >> i) & 1u)) vr[i] = typename KV::Raw{};
       }
     }
     // V for P.V: fp32 rows (vf), or, on the packed path, element pairs across
@@ -375,7 +394,7 @@ void decode_kernel(const DecodeParams p) {
     if constexpr (PVP) {
       uint32_t vp[NI][VEC / 2];
 #pragma unroll
-      for (int i = 0; i < NI; ++i) KV::template to_pairs<kF16>(T.v[i], vp[i]);
+      for (int i = 0; i < NI; ++i) KV::template to_pairs<kF16>(vr[i], vp[i]);
 #pragma unroll
       for (int u = 0; u < NI / 2; ++u)
 #pragma unroll
@@ -385,7 +404,7 @@ void decode_kernel(const DecodeParams p) {
         }
     } else {
 #pragma unroll
-      for (int i = 0; i < NI; ++i) KV::widen(T.v[i], vf[i]);
+      for (int i = 0; i < NI; ++i) KV::widen(vr[i], vf[i]);
     }
     float pw[NI][GC];  // weights 2^(s - m) of each token and head
     if constexpr (PBC) {

@@ -526,3 +526,95 @@ def test_q_alignment(pa, dev, qt, G):
         q = buf[off:].view(qd.shape)
         for entry in ("v1", "v3auto", "v3s7"):
             close(to_host(run(pa, entry, q, k, v, bt, ctx, 0.125)), want)
+
+
+# Non-finite codes planted in pool slots no sequence attends: (NaN, +Inf) per KV
+# type as stored (fp16 0x7E00 / 0x7C00, bf16 0x7FC0 / 0x7F80, FP8 E4M3 0x7F / 0xFF,
+# which has no infinity, and fp32 NaN / Inf).
+_POISON = {"f16": (0x7E00, 0x7C00), "bf16": (0x7FC0, 0x7F80), "fp8": (0x7F, 0xFF),
+           "f32": (0x7FC00000, 0x7F800000)}
+
+
+def _poison_unattended(k, v, bt, ctx, BS, kind):
+    """Copies of k / v (stored arrays) and bt where every slot no live token
+    reads holds NaN or Inf: the rows past the context end in each sequence's
+    last page, and the whole of block 0, which is made unreferenced by
+    swapping it with a block no live page uses (the caller adds a spare)."""
+    k, v, bt = k.copy(), v.copy(), bt.copy()
+    nb = k.shape[0]
+    live = set()
+    for b, c in enumerate(ctx):
+        live.update(int(x) for x in bt[b, :max(0, -(-int(c) // BS))])
+    spare = next(i for i in range(nb) if i not in live)
+    for a in (k, v):
+        a[[0, spare]] = a[[spare, 0]]
+    bt = np.where(bt == 0, spare, np.where(bt == spare, 0, bt)).astype(np.int32)
+    bits = {1: np.uint8, 2: np.uint16, 4: np.uint32}[k.itemsize]
+    nan, inf = (bits(x) for x in _POISON[kind])
+    for a in (k, v):
+        raw = a.view(bits)
+        raw[0] = nan
+        raw[0, 1::3] = inf
+        for b, c in enumerate(ctx):
+            if c > 0 and c % BS:
+                blk = bt[b, (int(c) - 1) // BS]
+                raw[blk, int(c) % BS:] = nan
+                raw[blk, int(c) % BS + 1::2] = inf
+    return k, v, bt
+
+
+@pytest.mark.parametrize("kind,H,HKV,D,BS", [
+    ("f16", 12, 12, 64, 16),   # MHA: one head per work-group (small batch), four packed (256-way split)
+    ("f16", 4, 4, 32, 16),     # MHA 64-byte rows: two heads per work-group
+    ("f16", 8, 2, 128, 16),    # GQA-4: quad-shared softmax, packed P.V over fp16 pairs
+    ("bf16", 8, 2, 128, 16),   # GQA-4 over bf16 (fp32 P.V)
+    ("fp8", 8, 2, 128, 16),    # GQA-4 over FP8
+    ("fp8", 4, 4, 64, 16),     # FP8 MHA, two heads per work-group
+    ("f32", 8, 4, 64, 16),     # fp32 cache, GQA-2
+    ("bf16", 16, 2, 128, 16),  # GQA-8: matrix-core decode kernel
+    ("f16", 8, 2, 64, 5),      # general gather (BS not a multiple of the rows per load)
+])
+def test_unattended_slots_hold_nan(pa, dev, kind, H, HKV, D, BS):
+    """Slots that no live token reads may hold any bits (freed pages, an FP8
+    pool from torch.empty): NaN and Inf planted in the tail of every last page
+    and in an unreferenced block 0 must not reach any output.  Every decode
+    entry point (v1, v2, v3 with the auto plan and explicit splits), the fp32
+    prefill path and, for 16-bit caches, the MFMA prefill."""
+    ctx = [1, 17, 300, 1000, 2049, 37]
+    seed = D + H + BS
+    scale = 0.11
+    if kind == "fp8":
+        inp, k8, v8, _, _ = fp8_case(len(ctx), H, HKV, D, BS, ctx, seed=seed, k_scale=1.0, v_scale=1.0)
+        # fp8_case has no spare block: append one that no page references.
+        k8, v8 = np.concatenate([k8, k8[:1]]), np.concatenate([v8, v8[:1]])
+        k, v, bt = _poison_unattended(k8, v8, inp["bt"], inp["ctx"], BS, kind)
+        kref, vref, kvname = oracle.fp8_decode(k), oracle.fp8_decode(v), "f32"
+        kd, vd = fp8_dev(k, dev), fp8_dev(v, dev)
+        q = torch.from_numpy(inp["q_f32"]).to(dev)
+    else:
+        inp = decode_case(len(ctx), H, HKV, D, BS, ctx, seed=seed, kv=kind, extra_blocks=1)
+        k, v, bt = _poison_unattended(inp["k"], inp["v"], inp["bt"], inp["ctx"], BS, kind)
+        kref, vref, kvname = k, v, kind
+        kd, vd = to_dev(k, kind, dev), to_dev(v, kind, dev)
+        q = to_dev(inp["q"], inp["qt"], dev)
+    assert not np.isfinite(oracle.to_float(kref, kvname)[0]).any()
+    btd, ctxd = torch.from_numpy(bt).to(dev), torch.from_numpy(inp["ctx"]).to(dev)
+    want = oracle.decode(inp["q_f32"], kref, vref, bt, inp["ctx"], scale, kvname)
+    assert np.isfinite(want).all()
+    tol = dict(atol=ATOL32, rtol=RTOL32) if kind == "f32" else {}
+    for entry in ("v1", "v2", "v3auto", "v3s1", "v3s3", "v3s64", "v3s256"):
+        got = to_host(run(pa, entry, q, kd, vd, btd, ctxd, scale))
+        assert np.isfinite(got).all(), entry
+        close(got, want, **tol)
+    # Prefill of the last 3 positions of each sequence (chunked: ctx > S).
+    S = 3
+    qp = np.random.default_rng(seed).standard_normal((len(ctx), S, H, D), dtype=np.float32)
+    wantp = oracle.prefill(qp, kref, vref, bt, inp["ctx"], scale, kvname)
+    qpd = torch.from_numpy(qp).to(dev)
+    got = to_host(pa.paged_attention_prefill(qpd, kd, vd, btd, ctxd, scale))
+    assert np.isfinite(got).all()
+    close(got, wantp, **tol)
+    if kind in ("f16", "bf16"):
+        got = to_host(pa.paged_attention_prefill_wmma(qpd, kd, vd, btd, ctxd, scale))
+        assert np.isfinite(got).all()
+        close(got, wantp)
