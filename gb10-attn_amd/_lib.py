@@ -23,6 +23,7 @@ DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_F64, DTYPE_I32, DTYPE_I64, DTYPE_FP8 = r
 EXPORTS = (
     "pa_abi_version", "pa_last_error", "paged_attention", "paged_attention_v2",
     "paged_attention_v3", "paged_attention_v3_scaled", "paged_attention_v3_workspace_size",
+    "paged_attention_v3_noalloc",
     "pa_v3_partition", "pa_v3_reduce",
     "choose_num_splits", "choose_num_splits_for", "pa_plan_partitions",
     "paged_attention_prefill", "paged_attention_prefill_wmma", "paged_attention_prefill_varlen",
@@ -82,6 +83,8 @@ def lib() -> C.CDLL:
         f.argtypes = six + [C.c_double, i64, P, sz, P]
     L.paged_attention_v3_scaled.restype = C.c_int
     L.paged_attention_v3_scaled.argtypes = six + [C.c_double, C.c_double, C.c_double, i64, P, sz, P]
+    L.paged_attention_v3_noalloc.restype = C.c_int
+    L.paged_attention_v3_noalloc.argtypes = six + [C.c_double, i64, P]
     L.pa_v3_reduce.restype = C.c_int
     L.pa_v3_reduce.argtypes = [T, T, T, T, T, i64, P, sz, P]
     L.paged_attention_v3_workspace_size.restype = sz

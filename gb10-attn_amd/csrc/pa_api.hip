@@ -13,10 +13,17 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/pagedattn.h"
 #include "pa_common.hpp"
+
+// Split scratch of paged_attention_v3_noalloc: a fixed device array, one copy
+// per GPU, held until the process ends.  Host code never passes `scratch`
+// itself to a kernel (on the host it names a stand-in, not device memory):
+// its device address is read per device with hipGetSymbolAddress.
+static __device__ __align__(256) unsigned char scratch[PA_NOALLOC_SCRATCH_BYTES];
 
 namespace pa {
 hipError_t launch_decode_f16(const DecodeParams& p, int gc, hipStream_t stream);
@@ -116,6 +123,29 @@ int device_cu_count(int* cus) {
     return fail(PA_ERR_HIP, "cannot read the compute-unit count of device %d", dev);
   if (dev < 64) cached[dev].store(n, std::memory_order_relaxed);
   *cus = n;
+  return PA_OK;
+}
+
+// Device address of the current device's `scratch`, looked up once per
+// device (the first paged_attention_v3_noalloc call on it) with that device
+// current, and kept.
+constexpr int kMaxDevices = 64;
+struct ScratchSlot {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+int scratch_address(void** ptr) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return fail(PA_ERR_HIP, "no HIP device is available");
+  if (dev >= kMaxDevices) return fail(PA_ERR_UNSUPPORTED, "device %d: at most %d devices are served", dev, kMaxDevices);
+  ScratchSlot& s = g_scratch[dev];
+  std::call_once(s.once, [&s] { s.err = hipGetSymbolAddress(&s.ptr, HIP_SYMBOL(scratch)); });
+  if (s.err != hipSuccess || !s.ptr)
+    return fail(PA_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(s.err));
+  *ptr = s.ptr;
   return PA_OK;
 }
 
@@ -369,10 +399,11 @@ enum V3Phase { kBoth = 3, kPartition = 1, kReduce = 2 };
 int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const pa_tensor_t* v,
            const pa_tensor_t* bt, const pa_tensor_t* ctx, double scale, int64_t num_splits,
            void* ws, size_t ws_bytes, void* stream, int phases, double k_scale = 1.0,
-           double v_scale = 1.0) {
+           double v_scale = 1.0, bool noalloc = false) {
   DecodeArgs a;
   int rc = check_args(out, q, k, v, bt, ctx, scale, false, &a);
   if (rc) return rc;
+  if (noalloc) ws_bytes = PA_NOALLOC_SCRATCH_BYTES;  // the split scratch is this device's fixed array
   if (!std::isfinite(k_scale) || !std::isfinite(v_scale))
     return fail(PA_ERR_INVALID_ARGUMENT, "k_scale and v_scale must be finite");
   // Dequantisation scales of the cache (FP8): k_scale joins the softmax
@@ -383,6 +414,12 @@ int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const p
   Plan plan;
   if ((rc = make_plan(a.p, a.gc, dtype_bytes(a.kv_dtype), num_splits, &plan))) return rc;
   const size_t need = workspace_bytes_for(a.p.B, a.p.H, a.p.D, plan);
+  if (noalloc && need > ws_bytes)
+    return fail(PA_ERR_WORKSPACE,
+                "paged_attention_v3_noalloc: this call's split needs %zu bytes of scratch, more than the "
+                "fixed %zu (PA_NOALLOC_SCRATCH_BYTES); use paged_attention_v3 with a workspace",
+                need, ws_bytes);
+  if (noalloc && (rc = scratch_address(&ws))) return rc;
   if (need > 0 && (!ws || ws_bytes < need))
     return fail(PA_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need, ws ? ws_bytes : 0);
   if (need > 0 && (reinterpret_cast<uintptr_t>(ws) & 255) != 0)
@@ -543,6 +580,14 @@ int paged_attention_v3_scaled(pa_tensor_t* out, const pa_tensor_t* q, const pa_t
                               int64_t num_splits, void* workspace, size_t workspace_bytes, void* stream) {
   return run_v3(out, q, k_cache, v_cache, block_tables, context_lens, scale, num_splits, workspace,
                 workspace_bytes, stream, kBoth, k_scale, v_scale);
+}
+
+int paged_attention_v3_noalloc(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                               const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                               const pa_tensor_t* context_lens, double scale, int64_t num_splits,
+                               void* stream) {
+  return run_v3(out, q, k_cache, v_cache, block_tables, context_lens, scale, num_splits, nullptr, 0, stream,
+                kBoth, 1.0, 1.0, true);
 }
 
 int pa_v3_partition(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,

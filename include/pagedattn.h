@@ -191,6 +191,22 @@ int paged_attention_v3_scaled(pa_tensor_t* out, const pa_tensor_t* q, const pa_t
                               const pa_tensor_t* context_lens, double scale, double k_scale, double v_scale,
                               int64_t num_splits, void* workspace, size_t workspace_bytes, void* stream);
 
+/* paged_attention_v3 without a workspace and without any allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The split's partials go to a fixed device array of
+ * PA_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until the
+ * process ends; a call whose split needs more (see
+ * paged_attention_v3_workspace_size) fails with PA_ERR_WORKSPACE before any
+ * device work.  Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (different streams, or other threads) race, so
+ * serialise them.  Same arguments, plan and results as paged_attention_v3. */
+#define PA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int paged_attention_v3_noalloc(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                               const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                               const pa_tensor_t* context_lens, double scale, int64_t num_splits,
+                               void* stream);
+
 /* Variable-length (mixed decode + prefill) batches on the MFMA path.  The
  * reference's prefill takes q [B, S, H, D] with one S for every sequence
  * (kernels/paged_attn_prefill.cu:62-64 trailing-chunk semantics); here
