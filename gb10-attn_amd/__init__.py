@@ -6,7 +6,7 @@ csrc/ by build.py); this package is its torch-facing mirror.  Import name:
 gb10_attn_amd (the directory is gb10-attn_amd; __graft_entry__.load_package()
 registers it).
 """
-from ._lib import EXPORTS, LIB_PATH, PaTensor, check, last_error, lib  # noqa: F401
+from ._lib import EXPORTS, LIB_PATH, PaTensor, check, last_error, last_launch, lib  # noqa: F401
 from .ops import (choose_num_splits, choose_num_splits_for, paged_attention,  # noqa: F401
                   paged_attention_prefill, paged_attention_prefill_varlen, paged_attention_prefill_wmma,
                   paged_attention_v2,

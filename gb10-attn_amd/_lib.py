@@ -21,7 +21,7 @@ DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_F64, DTYPE_I32, DTYPE_I64, DTYPE_FP8 = r
 
 # Every symbol include/pagedattn.h declares.
 EXPORTS = (
-    "pa_abi_version", "pa_last_error", "paged_attention", "paged_attention_v2",
+    "pa_abi_version", "pa_last_error", "pa_last_launch", "paged_attention", "paged_attention_v2",
     "paged_attention_v3", "paged_attention_v3_scaled", "paged_attention_v3_workspace_size",
     "paged_attention_v3_noalloc",
     "pa_v3_partition", "pa_v3_reduce",
@@ -71,6 +71,8 @@ def lib() -> C.CDLL:
     L.pa_abi_version.argtypes = []
     L.pa_last_error.restype = C.c_char_p
     L.pa_last_error.argtypes = []
+    L.pa_last_launch.restype = C.c_char_p
+    L.pa_last_launch.argtypes = []
     six = [T, T, T, T, T, T]
     for n in ("paged_attention", "paged_attention_v2", "paged_attention_prefill",
               "paged_attention_prefill_wmma"):
@@ -105,6 +107,11 @@ def lib() -> C.CDLL:
 
 def last_error() -> str:
     return lib().pa_last_error().decode()
+
+
+def last_launch() -> str:
+    """Kernel instances the last launching call on this thread dispatched."""
+    return lib().pa_last_launch().decode()
 
 
 def check(rc: int) -> None:

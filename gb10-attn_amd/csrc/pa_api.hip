@@ -26,6 +26,19 @@
 static __device__ __align__(256) unsigned char scratch[PA_NOALLOC_SCRATCH_BYTES];
 
 namespace pa {
+// Kernel instances dispatched by the last launching call on this thread.
+thread_local std::string g_launches;
+
+void note_launch(const char* fmt, ...) {
+  char buf[160];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  if (!g_launches.empty()) g_launches += "; ";
+  g_launches += buf;
+}
+
 hipError_t launch_decode_f16(const DecodeParams& p, int gc, hipStream_t stream);
 hipError_t launch_decode_bf16(const DecodeParams& p, int gc, hipStream_t stream);
 hipError_t launch_decode_f32(const DecodeParams& p, int gc, hipStream_t stream);
@@ -149,27 +162,39 @@ int scratch_address(void** ptr) {
   return PA_OK;
 }
 
-// Tuning knobs of the partition planner, overridable for measurement sweeps.
+// Tuning constants of the partition planner (compile-time; a sweep build
+// overrides them with -D): target resident work-groups per CU; the shortest
+// partition worth a work-group and the longest (bounds ragged imbalance), in
+// tokens; the longest when the plan splits anyway and the VALU kernel serves
+// the group (finer balance for ragged batches, config 3: +4 %; the
+// matrix-core kernel, groups of 8+, amortises its set-up over the longer
+// one); and a fixed head packing (> 0: KV heads per work-group for packable
+// layouts, whatever the split; 0: the planner's choice).
+#ifndef PA_PLAN_WGS_PER_CU
+#define PA_PLAN_WGS_PER_CU 3
+#endif
+#ifndef PA_PLAN_MIN_PART
+#define PA_PLAN_MIN_PART 256
+#endif
+#ifndef PA_PLAN_MAX_PART
+#define PA_PLAN_MAX_PART 2048
+#endif
+#ifndef PA_PLAN_MAX_PART_SPLIT
+#define PA_PLAN_MAX_PART_SPLIT 1024
+#endif
+#ifndef PA_PLAN_PACK
+#define PA_PLAN_PACK 0
+#endif
 struct PlanKnobs {
-  int64_t wgs_per_cu = 3;   // target resident work-groups per CU
-  int64_t min_part = 256;   // shortest partition worth a work-group (tokens)
-  int64_t max_part = 2048;        // longest partition (bounds ragged imbalance)
-  int64_t max_part_split = 1024;  // the same when the plan splits anyway and the VALU kernel serves
-                                  // the group: finer balance for ragged batches (config 3: +4 %); the
-                                  // matrix-core kernel (groups of 8+) amortises its set-up over 2048
-  int64_t pack = 0;  // > 0: KV heads per work-group for packable layouts, whatever the split
+  int64_t wgs_per_cu = PA_PLAN_WGS_PER_CU;
+  int64_t min_part = PA_PLAN_MIN_PART;
+  int64_t max_part = PA_PLAN_MAX_PART;
+  int64_t max_part_split = PA_PLAN_MAX_PART_SPLIT;
+  int64_t pack = PA_PLAN_PACK;
 };
 
 const PlanKnobs& knobs() {
-  static const PlanKnobs k = [] {
-    PlanKnobs r;
-    if (const char* s = getenv("PA_PLAN_WGS_PER_CU")) r.wgs_per_cu = std::max(1L, atol(s));
-    if (const char* s = getenv("PA_PLAN_MIN_PART")) r.min_part = std::max(16L, atol(s));
-    if (const char* s = getenv("PA_PLAN_MAX_PART")) r.max_part = std::max(16L, atol(s));
-    if (const char* s = getenv("PA_PLAN_MAX_PART_SPLIT")) r.max_part_split = std::max(16L, atol(s));
-    if (const char* s = getenv("PA_PLAN_PACK")) r.pack = std::max(0L, atol(s));
-    return r;
-  }();
+  static constexpr PlanKnobs k{};
   return k;
 }
 
@@ -380,6 +405,7 @@ int hip_status(hipError_t e, const char* what) {
 int run_direct(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const pa_tensor_t* v,
                const pa_tensor_t* bt, const pa_tensor_t* ctx, double scale, bool prefill,
                void* stream) {
+  g_launches.clear();
   DecodeArgs a;
   int rc = check_args(out, q, k, v, bt, ctx, scale, prefill, &a);
   if (rc) return rc;
@@ -400,6 +426,7 @@ int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const p
            const pa_tensor_t* bt, const pa_tensor_t* ctx, double scale, int64_t num_splits,
            void* ws, size_t ws_bytes, void* stream, int phases, double k_scale = 1.0,
            double v_scale = 1.0, bool noalloc = false) {
+  g_launches.clear();
   DecodeArgs a;
   int rc = check_args(out, q, k, v, bt, ctx, scale, false, &a);
   if (rc) return rc;
@@ -458,6 +485,7 @@ int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const p
 // variable-length layout (rows cu[b] .. cu[b+1] of a packed [T, H, D] q/out).
 int run_prefill_mfma(DecodeArgs& a, const pa_tensor_t* q, const int32_t* cu, int64_t T, double scale,
                      void* stream) {
+  g_launches.clear();
   // kernels/paged_attn_wmma.cu:220-223 requires fp16; bf16 is served as well.
   if (a.kv_dtype != kF16 && a.kv_dtype != kBF16)
     return fail(PA_ERR_INVALID_ARGUMENT, "the MFMA path needs an fp16 or bf16 KV cache");
@@ -506,6 +534,8 @@ extern "C" {
 int pa_abi_version(void) { return PA_ABI_VERSION; }
 
 const char* pa_last_error(void) { return g_last_error.c_str(); }
+
+const char* pa_last_launch(void) { return pa::g_launches.c_str(); }
 
 int64_t choose_num_splits_for(int64_t num_seqs, int64_t num_heads, int64_t max_context,
                               int64_t num_compute_units) {
@@ -678,6 +708,7 @@ int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const
 
 int pa_write_kv(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tensor_t* key,
                 const pa_tensor_t* value, const pa_tensor_t* slot_mapping, void* stream) {
+  g_launches.clear();
   int rc;
   if ((rc = check_tensor(k_cache, "k_cache", 4, "[NB, BS, HKV, D]"))) return rc;
   if ((rc = check_tensor(v_cache, "v_cache", 4, "[NB, BS, HKV, D]"))) return rc;

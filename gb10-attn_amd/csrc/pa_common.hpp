@@ -119,6 +119,10 @@ struct WriteParams {
   FastDiv bs_div;
 };
 
+// Records the kernel instance a launcher is about to dispatch, as profilers
+// print its demangled name, for pa_last_launch() (host side, per thread).
+void note_launch(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
 // Host launchers (defined in the kernel translation units).
 hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int gc, hipStream_t stream);
 hipError_t launch_reduce(const ReduceParams& p, hipStream_t stream);

@@ -28,8 +28,7 @@
 
 #include "pa_device.hpp"
 
-// Loop-structure knobs (compile-time): K/V loads per lane per tile, whether
-// the next tile's loads are issued before the current tile is consumed, and
+// Loop-structure knobs (compile-time): K/V loads per lane per tile, and
 // whether K/V loads carry the non-temporal (streaming) hint.
 #ifndef PA_DECODE_NI
 #define PA_DECODE_NI 4
@@ -37,17 +36,11 @@
 #ifndef PA_DECODE_NI_MHA
 #define PA_DECODE_NI_MHA 2  // loads per lane per tile for one unpacked MHA head per work-group (config 2: +0.8 % over 4)
 #endif
-#ifndef PA_DECODE_PIPE
-#define PA_DECODE_PIPE 1
-#endif
 #ifndef PA_DECODE_NT
 #define PA_DECODE_NT 1
 #endif
 #ifndef PA_DECODE_WAVES
 #define PA_DECODE_WAVES 4
-#endif
-#ifndef PA_DECODE_PRIO
-#define PA_DECODE_PRIO 0
 #endif
 #ifndef PA_DECODE_LAZY
 #define PA_DECODE_LAZY 1  // raise the softmax reference point only by more than 2^8
@@ -70,24 +63,13 @@
 
 namespace pa {
 
-template <typename KV, typename = void>
-struct requires_ni : std::false_type {};
-template <typename KV>
-struct requires_ni<KV, std::void_t<decltype(KV::kNI)>> : std::true_type {};
-
-template <typename KV>
-constexpr int kni() {
-  if constexpr (requires_ni<KV>::value) return KV::kNI > 0 ? KV::kNI : PA_DECODE_NI;
-  return PA_DECODE_NI;
-}
-
 template <typename KV, int D, int NIO = 0>
 struct DecodeShape {
   static constexpr int VEC = KV::kVec;         // elements per lane per load
   static constexpr int LPT = D / VEC;          // lanes per token row
   static_assert(LPT >= 1 && LPT <= 64 && (LPT & (LPT - 1)) == 0, "unsupported D/KV combination");
   static constexpr int TPI = 64 / LPT;         // token rows per load instruction
-  static constexpr int NI = NIO > 0 ? NIO : kni<KV>();  // K (and V) loads per lane per tile
+  static constexpr int NI = NIO > 0 ? NIO : PA_DECODE_NI;  // K (and V) loads per lane per tile
   static constexpr int TT = NI * TPI;          // tokens per wave tile
 };
 
@@ -282,7 +264,7 @@ void decode_kernel(const DecodeParams p) {
     T.live = live;
     // Keep the loads here: the scheduler would otherwise sink them next to
     // their uses (to save registers) and serialise memory behind compute.
-    if constexpr (PA_DECODE_PIPE) __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   // Fast gather.  When BS is a multiple of TPI and tiles start on multiples
@@ -318,7 +300,7 @@ void decode_kernel(const DecodeParams p) {
       live |= (okb && ti + slot < ct1) ? (1u << i) : 0u;
     }
     T.live = live;
-    if constexpr (PA_DECODE_PIPE) __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   // Online-softmax update of this lane group's streams with one tile.
@@ -374,18 +356,16 @@ void decode_kernel(const DecodeParams p) {
     // A masked token has weight 0, but its V row may be the rest of the last
     // page past the context end, or row `slot` of block 0 substituted for a
     // token past the partition, and either may hold any bits: 0 * NaN is NaN.
-    // On tiles with a masked token (a wave-uniform test, so full tiles pay
-    // one ballot) those rows are zeroed before P.V; all-zero bits are +0 in
-    // every KV type.
+    // Those rows are zeroed before P.V, one select per raw word (all-zero
+    // bits are +0 in every KV type).  Unconditional selects: a wave-uniform
+    // branch around them measured cheaper in instructions but cost 20-30
+    // registers (and an occupancy step) in most kernels.
     typename KV::Raw vr[NI];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) vr[i] = T.v[i];
-    if (__builtin_amdgcn_ballot_w64(T.live != (1u << NI) - 1u) != 0) {
-      asm volatile("");  // keep this a branch: full tiles skip the selects
+    for (int i = 0; i < NI; ++i) {
+      const bool lv = (T.live >> i) & 1u;
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        if (!((T.live >> i) & 1u)) vr[i] = typename KV::Raw{};
-      }
+      for (int w = 0; w < (int)(sizeof(vr[i]) / 4); ++w) vr[i][w] = lv ? T.v[i][w] : 0u;
     }
     // V for P.V: fp32 rows (vf), or, on the packed path, element pairs across
     // two tokens (vlo: element 2w of tokens 2u and 2u+1, vhi: element 2w+1).
@@ -522,30 +502,18 @@ void decode_kernel(const DecodeParams p) {
       auto sweep = [&](auto&& iss) {
         constexpr int kStep = NW * TT;
         const int first = ct0 + wave * TT;
-        if constexpr (!PA_DECODE_PIPE) {
-          for (int tile = first; tile < ct1; tile += kStep) {
-            Tile A;
-            iss(tile, cp, ct1, A);
-            consume(A);
-          }
-        } else if (first < ct1) {
+        if (first < ct1) {
           // Counted, branch-free body: tile j+1 is issued before tile j is
           // consumed.  Every entry of the loop header has exactly one tile
           // (in A) outstanding, so the waits stay partial.
           const int ntw = (ct1 - first + kStep - 1) / kStep;  // tiles of this wave
           Tile A, B;
           int tile = first;
-          if constexpr (PA_DECODE_PRIO) __builtin_amdgcn_s_setprio(3);
           iss(tile, cp, ct1, A);
-          if constexpr (PA_DECODE_PRIO) __builtin_amdgcn_s_setprio(0);
           for (int j = 0; j + 1 < ntw; j += 2) {
-            if constexpr (PA_DECODE_PRIO) __builtin_amdgcn_s_setprio(3);
             iss(tile + kStep, cp, ct1, B);
-            if constexpr (PA_DECODE_PRIO) __builtin_amdgcn_s_setprio(0);
             consume(A);
-            if constexpr (PA_DECODE_PRIO) __builtin_amdgcn_s_setprio(3);
             iss(tile + 2 * kStep, cp, ct1, A);
-            if constexpr (PA_DECODE_PRIO) __builtin_amdgcn_s_setprio(0);
             consume(B);
             tile += 2 * kStep;
           }
@@ -650,6 +618,7 @@ hipError_t launch_decode_dg(const DecodeParams& p, hipStream_t stream) {
   constexpr int PTS = PA_DECODE_DOT2 ? pair_types<KV>::value : 0;
   if constexpr ((PTS >> kF16) & 1) {
     if (p.q_dtype == kF16) {
+      note_launch("pa::decode_kernel<%s, %d, %d, %d, %d>", KV::kName, D, GC, HP, (int)kF16);
       hipLaunchKernelGGL((decode_kernel<KV, D, GC, HP, kF16>), dim3((unsigned)blocks), dim3(kDecodeThreads), 0,
                          stream, p);
       return hipGetLastError();
@@ -657,11 +626,13 @@ hipError_t launch_decode_dg(const DecodeParams& p, hipStream_t stream) {
   }
   if constexpr ((PTS >> kBF16) & 1) {
     if (p.q_dtype == kBF16) {
+      note_launch("pa::decode_kernel<%s, %d, %d, %d, %d>", KV::kName, D, GC, HP, (int)kBF16);
       hipLaunchKernelGGL((decode_kernel<KV, D, GC, HP, kBF16>), dim3((unsigned)blocks), dim3(kDecodeThreads), 0,
                          stream, p);
       return hipGetLastError();
     }
   }
+  note_launch("pa::decode_kernel<%s, %d, %d, %d, 0>", KV::kName, D, GC, HP);
   hipLaunchKernelGGL((decode_kernel<KV, D, GC, HP>), dim3((unsigned)blocks), dim3(kDecodeThreads), 0,
                      stream, p);
   return hipGetLastError();

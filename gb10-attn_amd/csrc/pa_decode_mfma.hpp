@@ -424,6 +424,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(const DecodeParams p) 
 template <typename KV, int D, int GC>
 hipError_t launch_decode_mfma_dg(const DecodeParams& p, hipStream_t stream) {
   const int64_t blocks = (int64_t)p.B * p.Sq * p.HKV * p.head_chunks * p.parts;
+  note_launch("pa::decode_mfma_kernel<%s, %d, %d>", KV::kName, D, GC);
   hipLaunchKernelGGL((decode_mfma_kernel<KV, D, GC>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
   return hipGetLastError();
 }

@@ -21,6 +21,7 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 // FP8: 8 bytes) and widened to fp32 in registers.
 
 struct KvF16 {
+  static constexpr const char* kName = "pa::KvF16";
   using Raw = u32x4_t;
   static constexpr int kBytes = 2;
   static constexpr int kVec = 8;
@@ -40,6 +41,7 @@ struct KvF16 {
 };
 
 struct KvBF16 {
+  static constexpr const char* kName = "pa::KvBF16";
   using Raw = u32x4_t;
   static constexpr int kBytes = 2;
   static constexpr int kVec = 8;
@@ -60,6 +62,7 @@ struct KvBF16 {
 };
 
 struct KvF32 {
+  static constexpr const char* kName = "pa::KvF32";
   using Raw = u32x4_t;
   static constexpr int kBytes = 4;
   static constexpr int kVec = 4;
@@ -74,6 +77,7 @@ struct KvF32 {
 };
 
 struct KvF64 {
+  static constexpr const char* kName = "pa::KvF64";
   using Raw = u32x4_t;
   static constexpr int kBytes = 8;
   static constexpr int kVec = 2;
@@ -87,20 +91,14 @@ struct KvF64 {
 };
 
 // OCP FP8 E4M3 ("e4m3fn": no infinities, S.1111.111 = NaN); v_cvt_pk_f32_fp8
-// widens two at a time (exact: every code is an fp32 value).  PA_FP8_WIDE
-// selects 16-byte lane loads (16 elements per lane) over 8-byte ones.
-#ifndef PA_FP8_WIDE
-#define PA_FP8_WIDE 0
-#endif
-#ifndef PA_FP8_NI
-#define PA_FP8_NI 0
-#endif
+// widens two at a time (exact: every code is an fp32 value).  Lanes load 8
+// bytes (8 elements), so per-lane state matches the 16-bit caches.
 struct KvFP8 {
+  static constexpr const char* kName = "pa::KvFP8";
   static constexpr int kBytes = 1;
-  static constexpr int kVec = PA_FP8_WIDE ? 16 : 8;
+  static constexpr int kVec = 8;
   static constexpr int kCode = kFP8;
-  static constexpr int kNI = PA_FP8_NI;  // loads per lane per tile (0: the default)
-  using Raw = typename std::conditional<PA_FP8_WIDE, u32x4_t, u32x2_t>::type;
+  using Raw = u32x2_t;
   __device__ static inline void widen(const Raw& r, float (&o)[kVec]) {
 #pragma unroll
     for (int w = 0; w < kVec / 4; ++w) {

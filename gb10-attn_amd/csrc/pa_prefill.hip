@@ -703,6 +703,7 @@ static hipError_t launch_pf_q(const PrefillParams& p, hipStream_t stream) {
   int64_t cus = 0, per_cu = 0;
   residency(kernel, cache, &cus, &per_cu);
   q.wg_cus = units > cus && units <= cus * per_cu ? (int32_t)cus : 0;  // one resident wave
+  note_launch("pa::prefill_mfma_kernel<%s, %d, %s>", KV::kName, D, kSplitQ ? "true" : "false");
   hipLaunchKernelGGL(kernel, dim3((unsigned)units), dim3(kPfThreads), 0, stream, q);
   return hipGetLastError();
 }

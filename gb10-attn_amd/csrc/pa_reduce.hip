@@ -139,6 +139,7 @@ hipError_t launch_reduce(const ReduceParams& p, hipStream_t stream) {
   const int64_t waves = (int64_t)p.B * p.H;
   const dim3 grid((unsigned)((waves + kReduceWaves - 1) / kReduceWaves));
   const dim3 block(64 * kReduceWaves);
+  note_launch("pa::reduce_kernel<%d>", p.D);
   switch (p.D) {
     case 32: hipLaunchKernelGGL(reduce_kernel<32>, grid, block, 0, stream, p); break;
     case 64: hipLaunchKernelGGL(reduce_kernel<64>, grid, block, 0, stream, p); break;

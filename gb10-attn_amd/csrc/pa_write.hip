@@ -106,6 +106,7 @@ template <int SRC, int DST>
 static hipError_t launch_w(const WriteParams& p, hipStream_t stream) {
   const int64_t work = (int64_t)p.T * p.HKV * (p.D >> 3);
   const unsigned blocks = (unsigned)((work + kWriteThreads - 1) / kWriteThreads);
+  note_launch("pa::write_kv_kernel<%d, %d, %s>", SRC, DST, p.slot_i64 ? "true" : "false");
   if (p.slot_i64)
     hipLaunchKernelGGL((write_kv_kernel<SRC, DST, true>), dim3(blocks), dim3(kWriteThreads), 0, stream, p);
   else

@@ -87,6 +87,12 @@ int pa_abi_version(void);
 /* Message for the last failed call on this thread ("" if none). */
 const char* pa_last_error(void);
 
+/* Kernel instances the last launching call on this thread dispatched, named
+ * as profilers print them (e.g. "pa::decode_kernel<pa::KvF16, 64, 1, 1, 1>"),
+ * separated by "; " ("" when that call launched nothing).  A diagnostic with
+ * no reference counterpart: it lets a benchmark report the kernel it timed. */
+const char* pa_last_launch(void);
+
 /* Decode, naive-fused semantics.  Replaces paged_attention(),
  * kernels/paged_attn_v1.h:13-15 (kernels/paged_attn_v1.cu:112-159).
  * q [B,H,D] f32|f16|bf16; k/v [NB,BS,HKV,D] f32|f16|bf16|f64; out [B,H,D] f32|f16|bf16. */
