@@ -63,7 +63,7 @@ class DecodeWorkload:
     """Paged decode with `pools` disjoint K/V pools, each holding every page of the batch."""
 
     def __init__(self, pa, *, B, H, HKV, D, BS, ctx, dtype, pools, seed, name, q_dtype=None,
-                 out_dtype=None, pool_tensor=None, kv_scale=None):
+                 out_dtype=None, pool_tensor=None, kv_scale=None, num_splits=0):
         self.pa, self.name = pa, name
         self.kv_scale = kv_scale  # quantised (FP8) cache: it holds N(0,1) / kv_scale
         self.B, self.H, self.HKV, self.D, self.BS = B, H, HKV, D, BS
@@ -85,7 +85,7 @@ class DecodeWorkload:
                 k = (torch.randn((nb, BS, HKV, D), generator=g, device=dev, dtype=torch.float32) * inv).to(dtype)
                 v = (torch.randn((nb, BS, HKV, D), generator=g, device=dev, dtype=torch.float32) * inv).to(dtype)
             nbp = k.shape[0]
-            perm = rng.permutation(nbp)[:nb].astype(np.int32)
+            perm = self._tables(rng, nbp, nb, B, pages, p)
             bt = np.zeros((B, self.MB), np.int32)
             pos = 0
             for b in range(B):
@@ -102,7 +102,8 @@ class DecodeWorkload:
         self.scale = 1.0 / float(np.sqrt(D))
         self.pools = pools
         self.L = pa.lib()
-        ws = pa.workspace_size(self.q, self.k[0], self.bt[0], 0)
+        self.num_splits = num_splits
+        ws = pa.workspace_size(self.q, self.k[0], self.bt[0], num_splits)
         self.ws = torch.empty(max(ws, 256), dtype=torch.uint8, device=dev)
         self.ws_bytes = ws
         self.split = ws > 0
@@ -117,58 +118,91 @@ class DecodeWorkload:
         self.bytes = (self.kv_bytes + self.q.numel() * self.q.element_size()
                       + self.out.numel() * self.out.element_size() + B * self.MB * 4 + B * 4)
 
+    def _tables(self, rng, nbp, nb, B, pages, p):
+        """Physical blocks of pool p's pages: a random choice of nb of its nbp blocks."""
+        return rng.permutation(nbp)[:nb].astype(np.int32)
+
     def footprint_gb(self):
         return sum(t.numel() * t.element_size() for t in self.k + self.v) / 1e9
 
     def launch(self, i, stream, ev_mid=None):
         a = self.args[i % self.pools]
-        ws = self.ws.data_ptr()
+        ws, ns = self.ws.data_ptr(), self.num_splits
         if self.kv_scale:  # one call (partition and reduce): the timed kernel includes the reduce
-            rc = self.L.paged_attention_v3_scaled(*a, self.scale, self.kv_scale, self.kv_scale, 0, ws,
+            rc = self.L.paged_attention_v3_scaled(*a, self.scale, self.kv_scale, self.kv_scale, ns, ws,
                                                   self.ws_bytes, stream)
             if rc == 0 and ev_mid is not None:
                 ev_mid.record()
         elif not self.split:
-            rc = self.L.paged_attention_v3(*a, self.scale, 0, ws, self.ws_bytes, stream)
+            rc = self.L.paged_attention_v3(*a, self.scale, ns, ws, self.ws_bytes, stream)
         else:
-            rc = self.L.pa_v3_partition(*a, self.scale, 0, ws, self.ws_bytes, stream)
+            rc = self.L.pa_v3_partition(*a, self.scale, ns, ws, self.ws_bytes, stream)
             if rc == 0 and ev_mid is not None:
                 ev_mid.record()
             if rc == 0:
-                rc = self.L.pa_v3_reduce(a[0], a[1], a[2], a[4], a[5], 0, ws, self.ws_bytes, stream)
+                rc = self.L.pa_v3_reduce(a[0], a[1], a[2], a[4], a[5], ns, ws, self.ws_bytes, stream)
         if rc != 0:
             raise RuntimeError(self.pa.last_error())
+
+
+class SweepWorkload(DecodeWorkload):
+    """GPT-2 decode (H=12, D=64, BS=16, fp16) at batch B and context ctx through
+    paged_attention_v3 with the library's plan: the small-batch / short-context
+    cold sweep of the reference (harness/gb10_burst.sh:103-116).  One shared
+    pool of at least 4x the 256 MB Infinity Cache, cut into disjoint block-table
+    sets used in rotation, one per step (the reference's --cold-pools)."""
+
+    def __init__(self, pa, pool, *, B, ctx, seed):
+        k, v = pool
+        BS = k.shape[1]
+        per_call = B * (-(-ctx // BS))
+        sets = max(1, min(k.shape[0] // per_call, 4096))
+        self._sets, self._per_call = sets, per_call
+        super().__init__(pa, B=B, H=12, HKV=12, D=64, BS=BS, ctx=[ctx] * B, dtype=torch.float16, pools=sets,
+                         seed=seed, name=f"sweep_b{B}_c{ctx}", pool_tensor=lambda p: (k, v))
+
+    def _tables(self, rng, nbp, nb, B, pages, p):
+        if p == 0:
+            self._perm = rng.permutation(nbp).astype(np.int32)
+        return self._perm[p * nb:(p + 1) * nb]
+
+    def footprint_gb(self):
+        return self._sets * self._per_call * 2 * self.BS * self.HKV * self.D * 2 / 1e9
 
 
 # ----------------------------------------------------------------- prefill --
 
 class PrefillWorkload:
-    """Causal paged prefill: K/V of S prompt tokens written into a paged pool, then attended."""
+    """Causal paged prefill: the K/V of a ctx-token prompt written into a paged
+    pool, then the last S positions attended (ctx = S: a whole prompt; ctx > S:
+    a trailing chunk, kernels/paged_attn_prefill.cu:62-64)."""
 
-    def __init__(self, pa, *, B, S, H, HKV, D, BS, dtype, seed, name):
+    def __init__(self, pa, *, B, S, H, HKV, D, BS, dtype, seed, name, ctx=None):
         self.pa, self.name = pa, name
+        ctx = ctx or S
         dev = torch.device("cuda:0")
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
-        pages = -(-S // BS)
+        pages = -(-ctx // BS)
         nb = B * pages
         rng = np.random.default_rng(seed)
         perm = rng.permutation(nb).astype(np.int32).reshape(B, pages)
         self.q = torch.randn((B, S, H, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
-        k_new = torch.randn((B, S, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
-        v_new = torch.randn((B, S, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+        k_new = torch.randn((B, ctx, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+        v_new = torch.randn((B, ctx, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
         # Write the prompt's K/V into the paged pool with pa_write_kv (untimed setup).
         self.k = torch.zeros((nb, BS, HKV, D), device=dev, dtype=dtype)
         self.v = torch.zeros_like(self.k)
-        tok = torch.arange(S, device=dev)
+        tok = torch.arange(ctx, device=dev)
         bt = torch.from_numpy(perm).to(dev)
         slots = (bt[:, tok // BS].long() * BS + tok % BS).reshape(-1)
-        pa.write_kv(self.k, self.v, k_new.reshape(B * S, HKV, D), v_new.reshape(B * S, HKV, D), slots)
+        pa.write_kv(self.k, self.v, k_new.reshape(B * ctx, HKV, D), v_new.reshape(B * ctx, HKV, D), slots)
         self.bt = bt
-        self.ctx = torch.full((B,), S, dtype=torch.int32, device=dev)
+        self.ctx = torch.full((B,), ctx, dtype=torch.int32, device=dev)
         self.out = torch.empty((B, S, H, D), device=dev, dtype=dtype)
         self.scale = 1.0 / float(np.sqrt(D))
-        self.flops = 4.0 * D * H * B * S * (S + 1) / 2.0  # causal pairs, QK^T and PV
+        # Causal pairs, QK^T and PV: row r sees ctx - S + r + 1 keys.
+        self.flops = 4.0 * D * H * B * (S * (ctx - S) + S * (S + 1) / 2.0)
         self.dtype = dtype
         V = pa.view
         self._views = [V(self.out), V(self.q), V(self.k), V(self.v), V(self.bt), V(self.ctx)]
@@ -181,6 +215,131 @@ class PrefillWorkload:
             raise RuntimeError(self.pa.last_error())
 
 
+# -------------------------------------------------------- correctness gate --
+# Every workload is checked against the CPU oracle on a sample of its own
+# inputs before it is timed (the reference publishes no number for a path that
+# fails its check, docs/REPORT.md:41-43); a failing workload is reported as
+# FAILED with no value.
+
+ATOL, RTOL = 2e-3, 1e-2  # north-star tolerance for 16-bit data: |got - want| <= ATOL + RTOL |want|
+
+
+def _compare(got, want, what):
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    err = np.abs(got - want)
+    bad = ~(err <= ATOL + RTOL * np.abs(want))
+    bad &= ~(np.isnan(got) & np.isnan(want))
+    return {"what": what, "max_abs": float(np.nanmax(err)) if err.size else 0.0,
+            "outside_tol": int(bad.sum()), "ok": bool(not bad.any())}
+
+
+def _gather_pages(k, v, bt, ctx, BS, scale=None):
+    """Host fp32 copies of the pages the rows of bt read, and bt remapped to them."""
+    ctx = np.asarray(ctx, np.int64)
+    used = np.unique(np.concatenate([bt[i, :max(0, -(-int(c) // BS))] for i, c in enumerate(ctx)]))
+    remap = np.zeros(int(k.shape[0]), np.int64)
+    remap[used] = np.arange(used.size)
+    idx = torch.from_numpy(used).to(k.device)
+    kh, vh = k[idx].float(), v[idx].float()
+    if scale:
+        kh, vh = kh * scale, vh * scale
+    return kh.cpu().numpy(), vh.cpu().numpy(), np.ascontiguousarray(remap[bt].astype(np.int32))
+
+
+def check_decode(work, nseq=2):
+    """One v3 call on pool 0 (the plan the timed loop runs); the sampled
+    sequences (the longest and shortest, else the first and last) against the
+    oracle's cpu_reference restatement.  Also returns the dispatched kernels."""
+    import oracle
+    ctx = work.ctx_host
+    seqs = sorted({int(np.argmax(ctx)), int(np.argmin(ctx))} if ctx.min() != ctx.max() else {0, work.B - 1})[:nseq]
+    work.out.fill_(float("nan"))
+    a = work.args[0]
+    rc = work.L.paged_attention_v3_scaled(*a, work.scale, work.kv_scale or 1.0, work.kv_scale or 1.0, work.num_splits,
+                                          work.ws.data_ptr(), work.ws_bytes, torch.cuda.current_stream().cuda_stream)
+    if rc != 0:
+        raise RuntimeError(work.pa.last_error())
+    kernels = work.pa.last_launch()
+    torch.cuda.synchronize()
+    got = work.out[seqs].float().cpu().numpy()
+    k, v, bts = _gather_pages(work.k[0], work.v[0], work.bt_host[seqs], ctx[seqs], work.BS, work.kv_scale)
+    want = oracle.decode(work.q[seqs].float().cpu().numpy(), k, v, bts, ctx[seqs], work.scale, "f32")
+    return _compare(got, want, f"sequences {seqs}, all {work.H} heads, vs oracle.decode"), kernels
+
+
+def check_prefill(work, rows=(0, 1, 63, 64, 127, 128, 129, 511, -2, -1)):
+    """One call; sampled query rows of the first and last sequence against the
+    oracle's decode of each row's visible prefix (position ctx - S + r)."""
+    import oracle
+    work.out.fill_(float("nan"))
+    work.launch(0, torch.cuda.current_stream().cuda_stream)
+    kernels = work.pa.last_launch()
+    torch.cuda.synchronize()
+    B, S = work.q.shape[0], work.q.shape[1]
+    ctx = work.ctx.cpu().numpy()
+    bt = work.bt.cpu().numpy()
+    rs = sorted({r % S for r in rows})
+    bs = [b for b in (0, B - 1) for _ in rs]
+    rr = [r for _ in (0, B - 1) for r in rs]
+    pos = np.asarray([int(ctx[b]) - S + r for b, r in zip(bs, rr)], np.int32)
+    k, v, bts = _gather_pages(work.k, work.v, bt[bs], pos + 1, work.k.shape[1])
+    want = oracle.decode(work.q.float().cpu().numpy()[bs, rr], k, v, bts, pos + 1, work.scale, "f32")
+    got = work.out.float().cpu().numpy()[bs, rr]
+    return _compare(got, want, f"{len(rr)} query rows of sequences 0 and {B - 1} vs oracle.decode of their prefix"), kernels
+
+
+def check_write(work):
+    """One write (copy 0); sampled tokens' K and V rows read back from their
+    slots must equal the source rows bit for bit (same dtype: a copy)."""
+    slots, key, val, kc, vc, _ = work._keep[0]
+    kc.zero_()
+    vc.zero_()
+    work.launch(0, torch.cuda.current_stream().cuda_stream)
+    kernels = work.pa.last_launch()
+    torch.cuda.synchronize()
+    T = key.shape[0]
+    t = torch.tensor(sorted({0, 1, T // 3, T // 2, T - 2, T - 1}), device=key.device)
+    sl = slots[t].long()
+    blk, row = sl // work.BS, sl % work.BS
+    ok = bool(torch.equal(kc[blk, row], key[t]) and torch.equal(vc[blk, row], val[t]))
+    return {"what": f"{t.numel()} tokens' K/V rows at their slots vs the source rows, bit for bit",
+            "ok": ok}, kernels
+
+
+def check_mixed(w):
+    """The varlen call; the first and last decode rows and sampled rows of the
+    first and last prefill chunk against the oracle's decode of their prefix."""
+    import oracle
+    w.out.fill_(float("nan"))
+    w.launch(0, None)
+    kernels = w.pa.last_launch()
+    torch.cuda.synchronize()
+    ctx = w.ctx.cpu().numpy()
+    cu = w.cu.cpu().numpy()
+    bt = w.bt.cpu().numpy()
+    seqs, rows = [], []
+    for b in (0, w.nd - 1):
+        seqs.append(b)
+        rows.append(0)
+    for b in (w.nd, w.nd + w.npf - 1):
+        for r in (0, 1, w.chunk // 2, w.chunk - 1):
+            seqs.append(b)
+            rows.append(r)
+    qlen = np.diff(cu)
+    pos = np.asarray([int(ctx[b]) - int(qlen[b]) + r for b, r in zip(seqs, rows)], np.int32)
+    trow = [int(cu[b]) + r for b, r in zip(seqs, rows)]
+    k, v, bts = _gather_pages(w.k, w.v, bt[seqs], pos + 1, w.k.shape[1])
+    want = oracle.decode(w.q.float().cpu().numpy()[trow], k, v, bts, pos + 1, w.scale, "f32")
+    got = w.out.float().cpu().numpy()[trow]
+    return _compare(got, want, f"{len(trow)} rows (decode rows and prefill-chunk rows) vs oracle.decode"), kernels
+
+
+def failed_record(name, check, kernels=None):
+    log(f"bench: {name} FAILED its correctness check: {check}")
+    return {"workload": name, "status": "FAILED", "check": check, "kernels": kernels}
+
+
 # ------------------------------------------------------------------ timing --
 
 class WriteWorkload:
@@ -189,7 +348,7 @@ class WriteWorkload:
     (source, pool) pairs so each step reads and writes HBM, not cache."""
 
     def __init__(self, pa, *, B, S, HKV, D, BS, dtype, seed, name, copies=8):
-        self.pa, self.name, self.dtype = pa, name, dtype
+        self.pa, self.name, self.dtype, self.BS = pa, name, dtype, BS
         dev = torch.device("cuda:0")
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
@@ -219,6 +378,15 @@ class WriteWorkload:
             raise RuntimeError(self.pa.last_error())
 
 
+# Configs 4a and 4b (whole prompts, S = ctx) and the reference's own prefill
+# shape: a 512-token chunk at context 2048, B = 4, GPT-2 heads, fp16
+# (results/c001-20260901-223111/bench_prefill.txt:40-42).
+PREFILL_CFG = {
+    "prefill_c4a": dict(B=8, S=1024, H=12, HKV=12, D=64, dtype=torch.float16, seed=4),
+    "prefill_c4b": dict(B=2, S=4096, H=32, HKV=32, D=128, dtype=torch.bfloat16, seed=6),
+    "prefill_ref_chunk": dict(B=4, S=512, ctx=2048, H=12, HKV=12, D=64, dtype=torch.float16, seed=7),
+}
+
 # The prompt K/V of configs 4a and 4b written into their paged pools.
 WRITE_CFG = {
     "write_kv_c4a": dict(B=8, S=1024, HKV=12, D=64, dtype=torch.float16, seed=14),
@@ -227,12 +395,16 @@ WRITE_CFG = {
 
 
 def write_record(work, steps, warmup):
+    chk, kernels = check_write(work)
+    if not chk["ok"]:
+        return failed_record(work.name, chk, kernels)
     ms, kms, _ = timed(work, steps, warmup)
     gbs = work.bytes / (kms * 1e-3) / 1e9
     return {
         "workload": work.name, "value": round(gbs, 1), "unit": "GB/s",
         "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4), "ms_per_step": round(ms, 5),
         "kernel_ms": round(kms, 5), "bytes_per_step": work.bytes, "dtype": str(work.dtype).replace("torch.", ""),
+        "kernels": kernels, "check": chk,
     }
 
 
@@ -283,6 +455,9 @@ class MixedWorkload:
 
 def mixed_record(pa, steps, warmup):
     w = MixedWorkload(pa)
+    chk, kernels = check_mixed(w)
+    if not chk["ok"]:
+        return failed_record(w.name, chk, kernels)
     ms, _, _ = timed(w, steps, warmup)
 
     class Split:
@@ -293,7 +468,7 @@ def mixed_record(pa, steps, warmup):
             "varlen_ms": round(ms, 5), "split_ms": round(ms_split, 5),
             "varlen_tokens_per_s": round(w.tokens / (ms * 1e-3), 1),
             "varlen_kv_GBs": round(w.kv_bytes / (ms * 1e-3) / 1e9, 1),
-            "flops_per_step": w.flops}
+            "flops_per_step": w.flops, "kernels": kernels, "check": chk}
 
 
 def call_overhead(pa, calls=3000):
@@ -339,6 +514,21 @@ def call_overhead(pa, calls=3000):
     with torch.cuda.graph(graph):
         ops.paged_attention_v3(q, k, v, bt, ctx, 0.125, 0)
     res["graph_replay_us"] = per_call(graph.replay)
+    # What a replay costs the runtime by itself: a graph of one trivial torch
+    # kernel, and the decode call's cost when 20 of them share one replay.
+    x = torch.zeros(1, device=dev)
+    tg = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        x.add_(1)
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(tg):
+        x.add_(1)
+    res["graph_replay_trivial_kernel_us"] = per_call(tg.replay)
+    g20 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g20):
+        for _ in range(20):
+            ops.paged_attention_v3(q, k, v, bt, ctx, 0.125, 0)
+    res["graph_of_20_calls_us_per_call"] = round(per_call(g20.replay) / 20, 2)
     return {"workload": "call_overhead", "unit": "us per call", "case": "v3 decode B=1 H=12 D=64 ctx=64 fp16",
             **res}
 
@@ -370,7 +560,7 @@ def timed(work, steps, warmup):
         work.launch(i, sp)
     torch.cuda.synchronize()
     split = getattr(work, "split", False)
-    reps, kern = [], []
+    reps, kern, tail = [], [], []
     n = warmup
     for r in range(REPEATS):
         t0 = torch.cuda.Event(enable_timing=True)
@@ -391,44 +581,70 @@ def timed(work, steps, warmup):
             ends[i].record(stream)
         torch.cuda.synchronize()
         kern += [starts[i].elapsed_time(mids[i] if split else ends[i]) for i in range(steps)]
+        if split:
+            tail += [mids[i].elapsed_time(ends[i]) for i in range(steps)]
         n += steps
     ms = float(np.median(reps))
+    # Split steps: the mean time from the partition kernel's end to the step's
+    # end (the reduce launch, plus the gap an event pair adds).
+    work.reduce_ms = float(np.mean(tail)) if split else None
     return ms, (float(np.mean(kern)) if split else ms), [round(x, 5) for x in reps]
 
 
-def traffic_from_profiles(kernel_key):
-    """HBM bytes per launch from the committed rocprofv3 counter summary, if present."""
+def traffic_from_profiles(workload, kernel, algorithmic_bytes):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary (profiles/traffic.json), with the reason when there is none: the
+    entry must name the kernel this run dispatched and the same algorithmic
+    bytes, else it describes another build or plan and is not used."""
     f = PROFILES / "traffic.json"
     if not f.exists():
-        return None
+        return None, "no profiles/traffic.json"
     try:
-        d = json.loads(f.read_text())
-        return d.get(kernel_key, {}).get("bytes_per_launch")
-    except (ValueError, OSError):
-        return None
+        d = json.loads(f.read_text()).get(workload)
+    except (ValueError, OSError) as e:
+        return None, f"profiles/traffic.json unreadable: {e}"
+    if not d:
+        return None, f"no counter entry for {workload}"
+    if d.get("kernel") != kernel:
+        return None, f"stale: the counters were taken on {d.get('kernel')}, this run dispatched {kernel}"
+    if abs(d.get("algorithmic_bytes", 0) - algorithmic_bytes) > 0.001 * algorithmic_bytes:
+        return None, "stale: the counters were taken on another workload size"
+    return d.get("bytes_per_launch"), "rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated (profiles/traffic.json)"
 
 
 # ------------------------------------------------------------- cpu baseline --
 
+def _llc_bytes():
+    """Total last-level cache of this host (sum over distinct L3 instances), or None."""
+    seen, total = set(), 0
+    base = Path("/sys/devices/system/cpu")
+    try:
+        for c in base.glob("cpu[0-9]*/cache/index3"):
+            key = (c / "shared_cpu_list").read_text().strip()
+            if key in seen:
+                continue
+            seen.add(key)
+            sz = (c / "size").read_text().strip()
+            total += int(sz[:-1]) * (1024 if sz.endswith("K") else 1024 * 1024) if sz[-1] in "KM" else int(sz)
+    except (OSError, ValueError):
+        return None
+    return total or None
+
+
 def cpu_baseline(work, seconds):
-    """The reference's scalar cpu_reference (oracle/_ref), one thread, on a sample of the
-    workload's sequences (all heads, full context), timed on this host.  Also checks the
-    GPU output of those sequences against it."""
+    """The reference's scalar cpu_reference (oracle/_ref), one thread, on ALL of
+    the workload's sequences (config 2: 64 x 12 heads x 2048 tokens, 805 MB of
+    fp32 K/V, far above the host's last-level cache, so it streams from DRAM as
+    the GPU's cold pools do), timed on this host.  Also checks every GPU output
+    row against it."""
     import oracle
     from oracle.pa_oracle import _p
     R = oracle.ref()
     kind = "reference" if R is not None else "port"
-    nsamp = 2
-    bt = work.bt_host[:nsamp]
-    used = np.unique(bt[bt >= 0])
-    remap = np.full(work.k[0].shape[0], -1, np.int64)
-    remap[used] = np.arange(used.size)
-    k = work.k[0][torch.from_numpy(used).to(work.k[0].device)].float().cpu().numpy()
-    v = work.v[0][torch.from_numpy(used).to(work.v[0].device)].float().cpu().numpy()
-    bts = np.ascontiguousarray(remap[bt].astype(np.int32))
-    ctx = np.ascontiguousarray(work.ctx_host[:nsamp])
-    q = np.ascontiguousarray(work.q[:nsamp].float().cpu().numpy())
-    B, H, D = q.shape
+    B, H, D = work.q.shape
+    k, v, bts = _gather_pages(work.k[0], work.v[0], work.bt_host, work.ctx_host, work.BS)
+    ctx = np.ascontiguousarray(work.ctx_host)
+    q = np.ascontiguousarray(work.q.float().cpu().numpy())
     NB, BS, HKV, _ = k.shape
     out = np.zeros((B, H, D), np.float32)
     if R is not None:
@@ -442,34 +658,34 @@ def cpu_baseline(work, seconds):
     torch.cuda.synchronize()
     work.launch(0, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
-    gpu = work.out[:nsamp].float().cpu().numpy()
-    err = float(np.abs(gpu - out).max())
-    ok = bool(np.allclose(gpu, out, atol=2e-3, rtol=1e-2))
+    gpu = work.out.float().cpu().numpy()
+    chk = _compare(gpu, out, "every GPU output row vs the reference's cpu_reference")
     n, t0 = 0, time.perf_counter()
     while True:
         run()
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds or n >= 10000:
+        if (el >= seconds and n >= 3) or n >= 10000:
             break
     if R is not None:
         R.ref_call_free(h)
     sample_bytes = 2.0 * float(ctx.sum()) * HKV * D * work.k[0].element_size()
     return {
         "value": round(sample_bytes * n / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
-        "sample": (f"{nsamp} of {work.B} sequences (all {work.H} heads, ctx {int(ctx[0])}), "
-                   f"{n} calls in {el:.1f} s; KV widened to fp32 for the reference's float API, "
-                   f"bytes counted at the GPU's {work.dtype} size"),
-        "check_vs_gpu": {"max_abs": err, "within_tol": ok},
+        "sample": (f"all {B} sequences (all {H} heads, ctx {int(ctx[0])}): {k.nbytes * 2 / 1e6:.0f} MB of fp32 K/V "
+                   f"per call (KV widened to fp32 for the reference's float API; bytes counted at the GPU's "
+                   f"{work.dtype} size), {n} calls in {el:.1f} s"),
+        "check_vs_gpu": {"max_abs": chk["max_abs"], "within_tol": chk["ok"]},
     }
 
 
-def simd_cpu(work, threads, seconds=2.0):
+def simd_cpu(work, threads, seconds=3.0):
     """Our SIMD/OpenMP port of cpu_reference (oracle/pa_oracle_simd.c, AVX2 + F16C),
-    parallel over (sequence, head) on `threads` host cores (BASELINE CPU path 2)."""
+    parallel over (sequence, head) on `threads` host cores (BASELINE CPU path 2),
+    on all of the workload's sequences in their storage type (config 2: 403 MB of
+    fp16 K/V per call, above the host's last-level cache)."""
     import oracle
-    nsamp = min(16, work.B)
-    bt = work.bt_host[:nsamp]
+    bt = work.bt_host
     used = np.unique(bt[bt >= 0])
     remap = np.full(work.k[0].shape[0], -1, np.int64)
     remap[used] = np.arange(used.size)
@@ -479,20 +695,20 @@ def simd_cpu(work, threads, seconds=2.0):
     k = np.ascontiguousarray(as_np(work.k[0][idx]))
     v = np.ascontiguousarray(as_np(work.v[0][idx]))
     bts = np.ascontiguousarray(remap[bt].astype(np.int32))
-    ctx = np.ascontiguousarray(work.ctx_host[:nsamp])
-    q = np.ascontiguousarray(work.q[:nsamp].float().cpu().numpy())
+    ctx = np.ascontiguousarray(work.ctx_host)
+    q = np.ascontiguousarray(work.q.float().cpu().numpy())
     run = lambda: oracle.decode_simd(q, k, v, bts, ctx, work.scale, tag, threads=threads)
     run()
     n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
+    while time.perf_counter() - t0 < seconds or n < 3:
         run()
         n += 1
     el = time.perf_counter() - t0
     sample_bytes = 2.0 * float(ctx.sum()) * work.HKV * work.D * work.k[0].element_size()
     return {"value": round(sample_bytes * n / el / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port_simd_openmp",
-            "sample": f"{nsamp} sequences (all heads), {n} calls in {el:.1f} s; the same sample each call "
-                      f"(host-cache resident)"}
+            "sample": f"all {work.B} sequences (all heads): {k.nbytes * 2 / 1e6:.0f} MB of {tag} K/V per call, "
+                      f"{n} calls in {el:.1f} s"}
 
 
 def host_info():
@@ -504,29 +720,37 @@ def host_info():
                 break
     except OSError:
         pass
-    return {"cpu": model, "nproc": os.cpu_count(), "threads_used": 16}
+    llc = _llc_bytes()
+    return {"cpu": model, "nproc": os.cpu_count(), "threads_used": 16,
+            "llc_MB_total": round(llc / 2**20, 1) if llc else None,
+            "note": "CPU samples stream their whole K/V set each call; every set exceeds the last-level cache"}
 
 
-def torch_sdpa_cpu(work, threads):
-    """PyTorch SDPA on the gathered paged layout, on the host CPU (BASELINE CPU path 3)."""
+def torch_sdpa_cpu(work, threads, seconds=3.0):
+    """PyTorch SDPA on the gathered paged layout, on the host CPU (BASELINE CPU
+    path 3), all of the workload's sequences (config 2: 805 MB of fp32 K/V per
+    call, above the host's last-level cache)."""
     torch.set_num_threads(threads)
-    nsamp = 2
-    idx = torch.from_numpy(work.bt_host[:nsamp].reshape(-1).astype(np.int64)).to(work.k[0].device)
-    k = work.k[0][idx].float().cpu().reshape(nsamp, -1, work.HKV, work.D)[:, :int(work.ctx_host[0])]
-    v = work.v[0][idx].float().cpu().reshape(nsamp, -1, work.HKV, work.D)[:, :int(work.ctx_host[0])]
-    q = work.q[:nsamp].float().cpu()[:, :, None, :]
+    ctx = int(work.ctx_host[0])
+    idx = torch.from_numpy(work.bt_host.reshape(-1).astype(np.int64)).to(work.k[0].device)
+    Bn = work.B
+    k = work.k[0][idx].float().cpu().reshape(Bn, -1, work.HKV, work.D)[:, :ctx]
+    v = work.v[0][idx].float().cpu().reshape(Bn, -1, work.HKV, work.D)[:, :ctx]
+    q = work.q.float().cpu()[:, :, None, :]
     kt = k.permute(0, 2, 1, 3).repeat_interleave(work.H // work.HKV, 1).contiguous()
     vt = v.permute(0, 2, 1, 3).repeat_interleave(work.H // work.HKV, 1).contiguous()
+    del k, v
     torch.nn.functional.scaled_dot_product_attention(q, kt, vt, scale=work.scale)
     n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < 2.0:
+    while time.perf_counter() - t0 < seconds or n < 3:
         torch.nn.functional.scaled_dot_product_attention(q, kt, vt, scale=work.scale)
         n += 1
     el = time.perf_counter() - t0
-    sample_bytes = 2.0 * nsamp * float(work.ctx_host[0]) * work.HKV * work.D * work.k[0].element_size()
+    sample_bytes = 2.0 * Bn * float(ctx) * work.HKV * work.D * work.k[0].element_size()
     return {"value": round(sample_bytes * n / el / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "torch_sdpa_gathered",
-            "sample": f"{nsamp} sequences gathered to fp32, {n} calls; the same sample each call (host-cache resident)"}
+            "sample": f"all {Bn} sequences gathered to fp32 ({(kt.nbytes + vt.nbytes) / 1e6:.0f} MB of K/V per "
+                      f"call), {n} calls in {el:.1f} s; bytes counted at the GPU's {work.dtype} size"}
 
 
 # --------------------------------------------------------------- workloads --
@@ -582,6 +806,10 @@ def make_c5(pa):
 
 
 def decode_record(work, steps, warmup):
+    """(ms, kernel ms, record), or (None, None, FAILED record) when the check fails."""
+    chk, kernels = check_decode(work)
+    if not chk["ok"]:
+        return None, None, failed_record(work.name, chk, kernels)
     ms, kms, reps = timed(work, steps, warmup)
     gbs = work.bytes / (ms * 1e-3) / 1e9
     return ms, kms, {
@@ -590,7 +818,110 @@ def decode_record(work, steps, warmup):
         "kernel_ms": round(kms, 5), "tokens_per_s": round(work.B / (ms * 1e-3), 1),
         "bytes_per_step": int(work.bytes), "split": work.split,
         "pools": work.pools, "footprint_GB": round(work.footprint_gb(), 2),
+        "kernels": kernels, "check": chk,
     }
+
+
+# The reference's v3 per-call times at the sweep's points, NVIDIA GB10
+# (results/c000-20260901-225701-verify/{cold,hot}_b{B}_c{ctx}.txt:19; the
+# "hot" points' working sets already exceed GB10's 24 MiB L2; b64_c2048 from
+# docs/REPORT.md:124, 402.65 MB / 231.3 GB/s).
+SWEEP_REF_US = {(1, 512): (21.7, "cold_b1_c512.txt:19"), (1, 2048): (34.4, "cold_b1_c2048.txt:19"),
+                (4, 512): (30.5, "cold_b4_c512.txt:19"), (4, 2048): (120.5, "cold_b4_c2048.txt:19"),
+                (16, 512): (116.7, "cold_b16_c512.txt:19"), (16, 2048): (464.2, "hot_b16_c2048.txt:19"),
+                (64, 512): (471.5, "hot_b64_c512.txt:19"), (64, 2048): (1740.8, "docs/REPORT.md:124"),
+                (128, 512): (907.8, "hot_b128_c512.txt:19")}
+
+
+def graph_us_per_call(work, calls):
+    """GPU time per call with host launch cost removed: `calls` consecutive
+    steps (rotating block-table sets) captured in one HIP graph, replayed."""
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(calls):
+            work.launch(i, s.cuda_stream)
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(g):
+        st = torch.cuda.current_stream().cuda_stream
+        for i in range(calls):
+            work.launch(i, st)
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 10
+    t0.record()
+    for _ in range(reps):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) * 1e3 / (reps * calls)
+
+
+def sweep_records(pa, steps):
+    """The reference's small-batch cold sweep, B in {1,4,16,64,128} x ctx in {512,2048}."""
+    dev = torch.device("cuda:0")
+    BS, H, D = 16, 12, 64
+    blk_bytes = BS * H * D * 2
+    nb = max(int(1.2e9 // (2 * blk_bytes)), 2 * 128 * 2048 // BS)  # >= 4x the Infinity Cache; 2 sets of the largest
+    g = torch.Generator(device=dev)
+    g.manual_seed(71)
+    k = torch.randn((nb, BS, H, D), generator=g, device=dev, dtype=torch.float32).half()
+    v = torch.randn((nb, BS, H, D), generator=g, device=dev, dtype=torch.float32).half()
+    out = []
+    for B in (1, 4, 16, 64, 128):
+        for ctx in (512, 2048):
+            w = SweepWorkload(pa, (k, v), B=B, ctx=ctx, seed=B * 10000 + ctx)
+            log(f"bench: sweep B={B} ctx={ctx} ({w._sets} block-table sets, {w.footprint_gb():.2f} GB)")
+            chk, kernels = check_decode(w)
+            if not chk["ok"]:
+                out.append(failed_record(w.name, chk, kernels))
+                continue
+            w.split = False  # time whole calls (partition + reduce)
+            ms, _, _ = timed(w, max(steps, 50), 10)
+            # The graph's calls cover >= 1.1 GB of distinct pages, so its replays stay cold too.
+            gus = graph_us_per_call(w, min(w._sets, max(4, -(-int(1.1e9) // int(w.bytes))), 1024))
+            ref_us, ref_src = SWEEP_REF_US.get((B, ctx), (None, None))
+            us = ms * 1e3
+            rec = {"workload": w.name, "batch": B, "context_len": ctx, "us_per_call": round(us, 2),
+                   "GBs": round(w.bytes / (us * 1e-6) / 1e9, 1),
+                   "frac_of_8TBs": round(w.bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                   "us_per_call_graph": round(gus, 2),
+                   "GBs_graph": round(w.bytes / (gus * 1e-6) / 1e9, 1),
+                   "frac_of_8TBs_graph": round(w.bytes / (gus * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                   "bytes_per_call": int(w.bytes), "split": w.ws_bytes > 0, "kernels": kernels,
+                   "block_table_sets": w._sets, "footprint_GB": round(w.footprint_gb(), 2), "check": chk}
+            if ref_us:
+                rec["reference_gb10_us"] = ref_us
+                rec["reference_source"] = "results/c000-20260901-225701-verify/" + ref_src \
+                    if ref_src.endswith(":19") else ref_src
+            out.append(rec)
+            del w
+    return out
+
+
+def c2_split_records(pa, pools, steps):
+    """Config 2 through the explicit split + LSE reduce: the reference's own
+    count (choose_num_splits on its 48-SM GB10: 64) and the fastest of a few
+    explicit counts, with the partition kernel and the reduce timed apart."""
+    recs = []
+    for ns in (64, 2, 4, 8, 16):
+        w = DecodeWorkload(pa, B=64, H=12, HKV=12, D=64, BS=16, ctx=[2048] * 64, dtype=torch.float16,
+                           pools=pools, seed=2, name=f"decode_c2_split{ns}", num_splits=ns)
+        log(f"bench: {w.name}")
+        ms, kms, rec = decode_record(w, max(20, steps), 5)
+        if ms is not None:
+            rec["num_splits"] = ns
+            rec["partition_kernel_ms"] = rec.pop("kernel_ms")
+            rec["reduce_ms"] = round(w.reduce_ms, 5)
+            rec["partition_kernel_GBs"] = round(w.bytes / (kms * 1e-3) / 1e9, 1)
+        recs.append(rec)
+        del w
+    ok = [r for r in recs[1:] if r.get("value")]
+    best = max(ok, key=lambda r: r["value"]) if ok else None
+    return [recs[0]] + ([dict(best, workload="decode_c2_split_best")] if best else [])
 
 
 _GEMM_REF = {}
@@ -625,6 +956,9 @@ def library_gemm_tflops(dtype, n=8192, reps=10):
 
 
 def prefill_record(work, steps, warmup):
+    chk, kernels = check_prefill(work)
+    if not chk["ok"]:
+        return failed_record(work.name, chk, kernels)
     ms, kms, _ = timed(work, steps, warmup)
     tf = work.flops / (kms * 1e-3) / 1e12
     gemm = library_gemm_tflops(work.dtype)
@@ -635,7 +969,7 @@ def prefill_record(work, steps, warmup):
         "ms_per_step": round(ms, 5),
         "kernel_ms": round(kms, 5), "flops_per_step": work.flops,
         "prompt_tokens_per_s": round(work.q.shape[0] * work.q.shape[1] / (ms * 1e-3), 1),
-        "dtype": str(work.dtype).replace("torch.", ""),
+        "dtype": str(work.dtype).replace("torch.", ""), "kernels": kernels, "check": chk,
     }
 
 
@@ -647,7 +981,7 @@ def main():
     ap.add_argument("--pools", type=int, default=6, help="rotated KV pools (config 2)")
     ap.add_argument("--workload", default="decode_c2",
                     choices=["decode_c2", "decode_c3", "decode_c5", "decode_c2_fp8", "decode_c3_fp8", "decode_gqa8",
-                             "prefill_c4a", "prefill_c4b",
+                             "decode_c2_split", "sweep", "prefill_c4a", "prefill_c4b", "prefill_ref_chunk",
                              "write_kv_c4a", "write_kv_c4b", "call_overhead", "mixed_c2", "copy_calib"],
                     help="with --only: run just this workload's kernel loop (for profiling)")
     ap.add_argument("--only", action="store_true", help="time only --workload, print its record")
@@ -678,11 +1012,14 @@ def main():
                               "bytes_written_per_copy": n, "copies": args.warmup + args.steps}), flush=True)
             return
         if w.startswith("prefill"):
-            work = (PrefillWorkload(pa, B=8, S=1024, H=12, HKV=12, D=64, BS=16, dtype=torch.float16, seed=4,
-                                    name="prefill_c4a") if w == "prefill_c4a" else
-                    PrefillWorkload(pa, B=2, S=4096, H=32, HKV=32, D=128, BS=16, dtype=torch.bfloat16,
-                                    seed=6, name="prefill_c4b"))
+            work = PrefillWorkload(pa, BS=16, name=w, **PREFILL_CFG[w])
             print(json.dumps(prefill_record(work, args.steps, args.warmup)), flush=True)
+        elif w == "sweep":
+            for rec in sweep_records(pa, args.steps):
+                print(json.dumps(rec), flush=True)
+        elif w == "decode_c2_split":
+            for rec in c2_split_records(pa, args.pools, args.steps):
+                print(json.dumps(rec), flush=True)
         elif w == "mixed_c2":
             print(json.dumps(mixed_record(pa, args.steps, args.warmup)), flush=True)
         elif w == "call_overhead":
@@ -707,32 +1044,39 @@ def main():
     log("bench: config 2 (GPT-2 decode, B=64 ctx=2048 fp16, rotated pools)")
     work = make_c2(pa, args.pools)
     ms, kms, rec = decode_record(work, args.steps, args.warmup)
+    base = {
+        "metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "higher_is_better": True, "scaling": "weak", "dtype": "f16",
+        "data": "synthetic N(0,1), seeded; random-permutation block tables",
+        "config": {"workload": "decode_c2", "batch": 64, "context_len": 2048, "heads": 12,
+                   "kv_heads": 12, "head_dim": 64, "block_size": 16, "kv_dtype": "f16",
+                   "q_dtype": "f16", "out_dtype": "f16", "entry": "paged_attention_v3(num_splits=0)",
+                   "pools": work.pools, "working_set_GB": round(work.footprint_gb(), 2),
+                   "split": work.split},
+    }
+    if ms is None:  # failed its correctness check: no number is published
+        print(json.dumps({**base, "value": None, "vs_baseline": None, "status": "FAILED", "check": rec["check"]}),
+              flush=True)
+        sys.exit(1)
     achieved = work.bytes / (kms * 1e-3) / 1e9
     log(f"bench: {rec['value']} GB/s per step, kernel {kms * 1e3:.1f} us")
-
+    kernel = rec["kernels"].split("; ")[0]
+    traffic, traffic_src = traffic_from_profiles("decode_c2", kernel, work.bytes)
     line = {
-        "metric": METRIC, "value": rec["value"], "unit": "GB/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        **base, "value": rec["value"], "ms_per_step": round(ms, 5),
         "timing": f"median of {REPEATS} repeats of {args.steps} steps", "repeats_ms": rec["repeats_ms"],
-        "higher_is_better": True, "scaling": "weak",
         "vs_baseline": round(rec["value"] / REF_GB10_C2_GBS, 2),
         "baseline": {"value": REF_GB10_C2_GBS, "unit": "GB/s", "frac_of_its_peak": 0.847,
                      "what": "reference v3 split decode, B=64 ctx=2048 fp16 (this config), on NVIDIA GB10 "
                              "(273 GB/s LPDDR5X): different hardware, compare frac_of_peak",
                      "source": "docs/REPORT.md:124"},
-        "dtype": "f16",
-        "data": "synthetic N(0,1), seeded; random-permutation block tables",
-        "config": {"workload": "decode_c2", "batch": 64, "context_len": 2048, "heads": 12,
-                   "kv_heads": 12, "head_dim": 64, "block_size": 16, "kv_dtype": "f16",
-                   "q_dtype": "f16", "out_dtype": "f16", "entry": "paged_attention_v3(num_splits=0)",
-                   "pools": work.pools, "working_set_GB": rec["footprint_GB"],
-                   "split": work.split},
         "frac_of_peak": rec["frac_of_8TBs"],
         "tokens_per_s": rec["tokens_per_s"],
+        "check": rec["check"],
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                     "traffic": traffic_from_profiles("decode_c2"),
-                     "kernel": "pa::decode_kernel<KvF16, 64, 1, 1, 1>",
+                     "traffic": traffic, "traffic_source": traffic_src,
+                     "kernel": kernel, "kernels_per_step": rec["kernels"],
                      "kernel_ms": round(kms, 5), "bytes_per_launch": int(work.bytes)},
     }
     log("bench: cpu baseline (reference cpu_reference, 1 thread)")
@@ -743,19 +1087,28 @@ def main():
 
     also = []
     if not args.no_also:
+        log("bench: config 2 through the explicit split + LSE reduce")
+        also += c2_split_records(pa, args.pools, max(20, args.steps // 4))
         for make in (lambda: make_c3(pa, 2), lambda: make_c5(pa), lambda: make_c2_fp8(pa, args.pools),
                      lambda: make_c3_fp8(pa, 2), lambda: make_gqa8(pa, 2)):
             w = make()
             log(f"bench: {w.name}")
-            also.append(decode_record(w, max(20, args.steps // 4), 5)[2])
+            rec = decode_record(w, max(20, args.steps // 4), 5)[2]
+            if rec.get("value") is not None:
+                rec["traffic"], rec["traffic_source"] = traffic_from_profiles(
+                    w.name, rec["kernels"].split("; ")[0], w.bytes)
             if w.name == "decode_c5":
-                also[-1]["k_base_offset_elements"] = int(w.k_offset_elems)
+                rec["k_base_offset_elements"] = int(w.k_offset_elems)
+            also.append(rec)
             del w
-        for name, kw in (("prefill_c4a", dict(B=8, S=1024, H=12, HKV=12, D=64, dtype=torch.float16, seed=4)),
-                         ("prefill_c4b", dict(B=2, S=4096, H=32, HKV=32, D=128, dtype=torch.bfloat16, seed=6))):
+        for name, kw in PREFILL_CFG.items():
             log(f"bench: {name}")
             w = PrefillWorkload(pa, BS=16, name=name, **kw)
-            also.append(prefill_record(w, max(20, args.steps // 4), 5))
+            rec = prefill_record(w, max(20, args.steps // 4), 5)
+            if name == "prefill_ref_chunk":
+                rec["reference_gb10_us"] = 6956.9
+                rec["reference_source"] = "results/c001-20260901-223111/bench_prefill.txt:42 (WMMA kernel)"
+            also.append(rec)
             del w
         for name, kw in WRITE_CFG.items():
             log(f"bench: {name}")
@@ -764,6 +1117,8 @@ def main():
             del w
         log("bench: mixed decode + prefill batch")
         also.append(mixed_record(pa, max(20, args.steps // 4), 5))
+        log("bench: small-batch cold sweep")
+        also += sweep_records(pa, max(50, args.steps // 4))
         log("bench: per-call host overhead")
         also.append(call_overhead(pa))
     line["also"] = also
