@@ -164,7 +164,8 @@ int scratch_address(void** ptr) {
 
 // Tuning constants of the partition planner (compile-time; a sweep build
 // overrides them with -D): target resident work-groups per CU; the shortest
-// partition worth a work-group and the longest (bounds ragged imbalance), in
+// partition worth a work-group (and the same for tiny grids, whose time is
+// latency, not bandwidth) and the longest (bounds ragged imbalance), in
 // tokens; the longest when the plan splits anyway and the VALU kernel serves
 // the group (finer balance for ragged batches, config 3: +4 %; the
 // matrix-core kernel, groups of 8+, amortises its set-up over the longer
@@ -175,6 +176,9 @@ int scratch_address(void** ptr) {
 #endif
 #ifndef PA_PLAN_MIN_PART
 #define PA_PLAN_MIN_PART 256
+#endif
+#ifndef PA_PLAN_MIN_PART_TINY
+#define PA_PLAN_MIN_PART_TINY 64
 #endif
 #ifndef PA_PLAN_MAX_PART
 #define PA_PLAN_MAX_PART 2048
@@ -188,6 +192,7 @@ int scratch_address(void** ptr) {
 struct PlanKnobs {
   int64_t wgs_per_cu = PA_PLAN_WGS_PER_CU;
   int64_t min_part = PA_PLAN_MIN_PART;
+  int64_t min_part_tiny = PA_PLAN_MIN_PART_TINY;
   int64_t max_part = PA_PLAN_MAX_PART;
   int64_t max_part_split = PA_PLAN_MAX_PART_SPLIT;
   int64_t pack = PA_PLAN_PACK;
@@ -365,7 +370,10 @@ int make_plan(const DecodeParams& p, int gc, int kv_bytes, int64_t num_splits, P
   }
   const int64_t nparts = parts_for(lo, &ptok);
   int hp = lo;
-  for (int c = hi; c > lo; c /= 2) {
+  // A grid that does not fill the GPU even unpacked keeps every work-group
+  // it can get (latency-bound: more loads in flight beat wider rows).
+  const bool fills = (int64_t)p.B * p.Sq * (p.HKV / lo) * nparts >= (int64_t)cus * knobs().wgs_per_cu;
+  for (int c = hi; fills && c > lo; c /= 2) {
     int64_t pt = 0;
     if (parts_for(c, &pt) == nparts && pt == ptok) {
       hp = c;
@@ -570,14 +578,20 @@ int pa_plan_partitions(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads
   int64_t S = (target + units - 1) / units;                             // fill the GPU
   const int64_t max_part = S > 1 && gc < 8 ? kn.max_part_split : kn.max_part;
   S = std::max(S, (max_context + max_part - 1) / max_part);             // bound partition length
-  S = std::min(S, std::max<int64_t>(1, max_context / kn.min_part));     // keep partitions long
+  // Tiny grids (the units with partitions of min_part tokens still cannot
+  // fill the GPU: a few short sequences) take shorter partitions, so that
+  // more work-groups have their loads in flight at once.
+  const bool tiny = units * std::max<int64_t>(1, max_context / kn.min_part) < target;
+  const int64_t min_part = tiny ? kn.min_part_tiny : kn.min_part;
+  S = std::min(S, std::max<int64_t>(1, max_context / min_part));        // keep partitions long enough
   if (S <= 1 || max_context <= 0) {
     *partition_tokens = std::max<int64_t>(max_context, 1);
     *num_partitions = 1;
     return PA_OK;
   }
   int64_t ptok = (max_context + S - 1) / S;
-  ptok = (ptok + 127) / 128 * 128;  // whole wave tiles for all 4 waves
+  const int64_t gran = ptok > 64 ? 128 : 64;  // whole wave tiles for all 4 waves
+  ptok = (ptok + gran - 1) / gran * gran;
   *partition_tokens = ptok;
   *num_partitions = (max_context + ptok - 1) / ptok;
   if (*num_partitions <= 1) *partition_tokens = std::max<int64_t>(max_context, 1);

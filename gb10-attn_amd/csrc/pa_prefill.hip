@@ -179,11 +179,23 @@ __device__ inline int swv(int row, int cc) {
   return row * D + (vpos<D>(row, cc) << 3);
 }
 
-template <typename KV, int D, bool kSplitQ>
+// kSplit (key-split mode, tiles of two 32-key m-tiles): a work-group serves
+// 64 query rows; waves 0-1 own rows 0-31 / 32-63 over the first 32 keys of
+// every tile, waves 2-3 the same rows over the second 32, and the two halves
+// are merged through LDS at the end (log-sum-exp rule).  The loads and the
+// LDS layout are those of the plain mode; each wave does half of a tile's
+// work, so a query block's chain of tiles takes half as long and twice as
+// many work-groups share the work.  Chosen when the plain grid is too short
+// for the dispatcher to balance causal blocks (config 4a: 768 work-groups,
+// chains of 2 to 16 tiles, on 768 slots).
+template <typename KV, int D, bool kSplitQ, bool kSplit>
 __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(PfShape<D>::WAVES_PER_EU)))
 void prefill_mfma_kernel(const PrefillParams p) {
   using Sh = PfShape<D>;
-  constexpr int QW = Sh::QW, QB = Sh::QB, KB = Sh::KB, MT = Sh::MT, KS = Sh::KS, DT = Sh::DT;
+  constexpr int QW = Sh::QW, KB = Sh::KB, MT = Sh::MT, KS = Sh::KS, DT = Sh::DT;
+  static_assert(!kSplit || MT == 2, "the key-split mode halves tiles of two m-tiles");
+  constexpr int MTW = kSplit ? 1 : MT;           // 32-key m-tiles of each tile this wave computes
+  constexpr int QB = kSplit ? 2 * QW : Sh::QB;   // query rows per work-group
   constexpr int NCH = Sh::NCH, CPT = Sh::CPT;
   constexpr bool kBf16 = KV::kCode == kBF16;
 
@@ -199,6 +211,8 @@ void prefill_mfma_kernel(const PrefillParams p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rw = kSplit ? (wave & 1) : wave;   // this wave's 32 query rows of the block
+  const int par = kSplit ? (wave >> 1) : 0;    // key half of every tile (key-split mode)
   const int n = lane & 31;   // query column of this lane (S^T, O^T) / key row (K operand)
   const int hh = lane >> 5;  // lane half: k-slot block of the operands
 
@@ -245,7 +259,7 @@ void prefill_mfma_kernel(const PrefillParams p) {
   const int maxctx = p.MB * p.BS;
   const int qs0 = qt * QB;
   if (qs0 >= Sr) return;            // no served rows of this sequence here (work-group uniform)
-  const int qw0 = qs0 + wave * QW;  // this wave's first query row
+  const int qw0 = qs0 + rw * QW;    // this wave's first query row
   const int qrow = qw0 + n;
   const bool live = qrow < Sr;
 
@@ -455,16 +469,21 @@ void prefill_mfma_kernel(const PrefillParams p) {
 
     // S^T, softmax and O^T update for tile t from LDS (cK, cV).
     auto compute = [&](int t, const uint16_t* cK, const uint16_t* cV) {
-      f32x16_t st[MT];
+      // Key-split mode: this wave's 32 keys are rows par*32 .. of the tile;
+      // the swizzles depend on row bits below 32 only, so its m-tile is the
+      // tile's shifted by par*32 rows.
+      cK += par * 32 * D;
+      cV += par * 32 * D;
+      f32x16_t st[MTW];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
+      for (int mt = 0; mt < MTW; ++mt) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) st[mt][r] = 0.0f;
       }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
+        for (int mt = 0; mt < MTW; ++mt) {
           const u32x4_t a = *reinterpret_cast<const u32x4_t*>(cK + swk<D>(mt * 32 + n, 2 * ks + hh));
           st[mt] = mfma32<kBf16>(a, qf[ks], st[mt]);
           if constexpr (kSplitQ) st[mt] = mfma32<kBf16>(a, qf_lo[ks], st[mt]);
@@ -473,12 +492,12 @@ void prefill_mfma_kernel(const PrefillParams p) {
       // Keys of this lane: t*KB + mt*32 + 8*(r/4) + 4*hh + r%4.  Only tiles
       // that cross the wave's diagonal (or the end of the keys) are masked;
       // the empty asm keeps this a branch rather than selects on every tile.
-      const int tk0 = t * KB;
-      if (tk0 + KB > wave_kfull) {
+      const int tk0 = t * KB + par * 32;
+      if (tk0 + MTW * 32 > wave_kfull) {
         asm volatile("");
         const int thr = qlim - tk0 - 4 * hh;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
+        for (int mt = 0; mt < MTW; ++mt) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             if (mt * 32 + 8 * (r >> 2) + (r & 3) > thr) st[mt][r] = -__builtin_inff();
@@ -491,7 +510,7 @@ void prefill_mfma_kernel(const PrefillParams p) {
       // on that (rare) branch.
       float mx = -__builtin_inff();
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
+      for (int mt = 0; mt < MTW; ++mt) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
       }
@@ -517,7 +536,7 @@ void prefill_mfma_kernel(const PrefillParams p) {
       const int trow = 4 * hh + (li >> 2);
       const int tcol = 16 * ((lane >> 4) & 1) + (li & 3) * 4;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
+      for (int mt = 0; mt < MTW; ++mt) {
         u32x4_t pb[2], pb_lo[kPvBf16 ? 2 : 1];
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -580,7 +599,7 @@ void prefill_mfma_kernel(const PrefillParams p) {
       if (t + 2 < ntiles) build(t + 2, s_off0);
       const bool more1 = t + 1 < ntiles;
       if (more1) issue(s_off1, sK1, sV1);
-      if (t * KB < wave_kend) compute(t, sK0, sV0);
+      if (t * KB + par * 32 < wave_kend) compute(t, sK0, sV0);
       if (more1) {
         __builtin_amdgcn_s_waitcnt(0x0F70);
         finish(sV1);
@@ -591,7 +610,7 @@ void prefill_mfma_kernel(const PrefillParams p) {
       if (t + 3 < ntiles) build(t + 3, s_off1);
       const bool more2 = t + 2 < ntiles;
       if (more2) issue(s_off0, sK0, sV0);
-      if ((t + 1) * KB < wave_kend) compute(t + 1, sK1, sV1);
+      if ((t + 1) * KB + par * 32 < wave_kend) compute(t + 1, sK1, sV1);
       if (t + 2 < ntiles) {
         __builtin_amdgcn_s_waitcnt(0x0F70);
         finish(sV0);
@@ -624,6 +643,36 @@ void prefill_mfma_kernel(const PrefillParams p) {
   if (badkey != 0x7fffffff) atomicMin(&s_badkey, badkey);
   __syncthreads();
   const int bad_from = s_badkey;
+
+  // Key-split mode: waves 2-3 hand their (m, l, O^T) to waves 0-1 through
+  // the (now idle) tile buffers; the lanes of the two waves hold the same
+  // rows and dims, so the merge is lane by lane (log-sum-exp rule on the
+  // reference points m, which are -inf where a wave saw no key).
+  if constexpr (kSplit) {
+    float* xo = reinterpret_cast<float*>(rw == 0 ? sK0 : sK1);  // [DT * 16][64]: KB * D halves hold it
+    float* xm = reinterpret_cast<float*>(sV0) + rw * 128;       // m [64], l [64]
+    if (par == 1) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xo[(dt * 16 + r) * 64 + lane] = o[dt][r];
+      }
+      xm[lane] = m;
+      xm[64 + lane] = l;
+    }
+    __syncthreads();
+    if (par == 1) return;
+    const float m2 = xm[lane], l2 = xm[64 + lane];
+    const float mn = fmaxf(m, m2);
+    const float a = m == -__builtin_inff() ? 0.0f : fast_exp2(m - mn);
+    const float c = m2 == -__builtin_inff() ? 0.0f : fast_exp2(m2 - mn);
+    l = l * a + l2 * c;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * a + xo[(dt * 16 + r) * 64 + lane] * c;
+    }
+  }
 
   // Row sum over the two lane halves, normalise, write.  O^T slot r of lane
   // (n, hh) in m-tile dt is dim dt*32 + 8*(r/4) + 4*hh + r%4 of row qrow.
@@ -694,25 +743,42 @@ static void residency(F kernel, std::atomic<int64_t> (&cache)[64], int64_t* cus,
   *per_cu = k;
 }
 
-template <typename KV, int D, bool kSplitQ>
+template <typename KV, int D, bool kSplitQ, bool kSplit>
 static hipError_t launch_pf_q(const PrefillParams& p, hipStream_t stream) {
   static std::atomic<int64_t> cache[64];
-  const auto kernel = prefill_mfma_kernel<KV, D, kSplitQ>;
+  const auto kernel = prefill_mfma_kernel<KV, D, kSplitQ, kSplit>;
   PrefillParams q = p;
+  constexpr int QB = kSplit ? 2 * PfShape<D>::QW : PfShape<D>::QB;
+  q.q_tiles = (p.S + QB - 1) / QB;
   const int64_t units = (int64_t)q.B * q.H * q.q_tiles;
   int64_t cus = 0, per_cu = 0;
   residency(kernel, cache, &cus, &per_cu);
   q.wg_cus = units > cus && units <= cus * per_cu ? (int32_t)cus : 0;  // one resident wave
-  note_launch("pa::prefill_mfma_kernel<%s, %d, %s>", KV::kName, D, kSplitQ ? "true" : "false");
+  note_launch("pa::prefill_mfma_kernel<%s, %d, %s, %s>", KV::kName, D, kSplitQ ? "true" : "false",
+              kSplit ? "true" : "false");
   hipLaunchKernelGGL(kernel, dim3((unsigned)units), dim3(kPfThreads), 0, stream, q);
   return hipGetLastError();
 }
 
+// Key-split mode when the plain grid (blocks of 128 query rows) has fewer
+// work-groups than CUs (PA_PF_SPLIT_BELOW per CU): chunks of a long context
+// (the reference's 512-token chunk at context 2048: 192 work-groups, +19 %).
+// Above that, twice the tiles cost more than the shorter chains save
+// (config 4a, 768 work-groups: -17 %).
+#ifndef PA_PF_SPLIT_BELOW
+#define PA_PF_SPLIT_BELOW 1
+#endif
 template <typename KV, int D>
 static hipError_t launch_pf(const PrefillParams& p, hipStream_t stream) {
-  PrefillParams q = p;
-  q.q_tiles = (p.S + PfShape<D>::QB - 1) / PfShape<D>::QB;
-  return p.q_split ? launch_pf_q<KV, D, true>(q, stream) : launch_pf_q<KV, D, false>(q, stream);
+  if constexpr (PfShape<D>::MT == 2) {
+    static std::atomic<int64_t> cache[64];
+    int64_t cus = 0, per_cu = 0;
+    residency(prefill_mfma_kernel<KV, D, false, false>, cache, &cus, &per_cu);
+    const int64_t plain = (int64_t)p.B * p.H * ((p.S + PfShape<D>::QB - 1) / PfShape<D>::QB);
+    if (cus > 0 && plain < PA_PF_SPLIT_BELOW * cus)
+      return p.q_split ? launch_pf_q<KV, D, true, true>(p, stream) : launch_pf_q<KV, D, false, true>(p, stream);
+  }
+  return p.q_split ? launch_pf_q<KV, D, true, false>(p, stream) : launch_pf_q<KV, D, false, false>(p, stream);
 }
 
 template <typename KV>

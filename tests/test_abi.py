@@ -184,10 +184,15 @@ def test_plan_partitions(pa):
     assert pa.plan_partitions(32, 64, 8, 128, 8192, 256) == (2048, 4)
     # tiny problem: no split
     assert pa.plan_partitions(1, 1, 1, 64, 100, 256) == (100, 1)
+    # tiny grids (a few short sequences, far from filling 256 CUs): 64- or 128-token partitions
+    # instead of 256, so that more work-groups stream at once (B=1 ctx=512: 8 x 64; B=4 ctx=2048: 16 x 128)
+    assert pa.plan_partitions(1, 12, 12, 64, 512, 256) == (64, 8)
+    assert pa.plan_partitions(4, 12, 12, 64, 2048, 256) == (128, 16)
+    assert pa.plan_partitions(16, 12, 12, 64, 2048, 256) == (512, 4)
     for B in (1, 2, 7, 64, 300):
         for ctx in (1, 31, 256, 4096, 100000):
             ptok, n = pa.plan_partitions(B, 32, 8, 128, ctx, 256)
-            assert n >= 1 and ptok * n >= ctx and (n == 1 or ptok % 128 == 0)
+            assert n >= 1 and ptok * n >= ctx and (n == 1 or ptok % 128 == 0 or ptok == 64)
             assert n == 1 or (n - 1) * ptok < ctx
     rc = pa.lib().pa_plan_partitions(1, 6, 4, 64, 10, 256, C.byref(C.c_int64()), C.byref(C.c_int64()))
     assert rc == 1

@@ -231,3 +231,22 @@ def test_varlen_malformed_ranges_and_max_q_len(pa, dev):
             want = oracle.prefill(q32[5:45][None], inp["k"], inp["v"], inp["bt"][1:2], inp["ctx"][1:2],
                                   0.125, "f16")[0]
             close(got[5:5 + 32], want[:32])
+
+
+@pytest.mark.parametrize("kv,qt", [("f16", "f16"), ("bf16", "bf16"), ("f16", "f32"), ("bf16", "f32")])
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_mfma_prefill_plain_and_key_split_modes(pa, dev, kv, qt, D):
+    """The MFMA prefill serves a grid of fewer work-groups than CUs in its
+    key-split mode (64 query rows per work-group, each tile's two 32-key
+    halves on different waves, merged through LDS) and larger grids in the
+    plain mode (128 rows, whole tiles).  The same causal + chunked shapes in
+    both modes (a few heads; many heads), against the oracle; the dispatched
+    kernel names the mode."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    h_plain = 2 * (-(-cus // 8))  # 2 sequences x 2 blocks of 128 rows x h_plain heads >= CUs
+    for H, split in ((4, True), (h_plain, False)):
+        inp = prefill_case(2, 200, H, 2, D, 16, [200, 500], seed=D + H, kv=kv, qt=qt)
+        got = pa.paged_attention_prefill_wmma(*dev_args(inp, dev), 1.0 / np.sqrt(D))
+        kern = pa.last_launch()
+        assert kern.endswith(", true>" if split else ", false>"), kern
+        close(to_host(got), want_of(inp, 1.0 / np.sqrt(D)))
