@@ -10,8 +10,10 @@ What pins each oracle function:
                       (one token, constant keys, zero scale); GQA == MHA on replicated
                       KV heads; block-permutation invariance.
   decode_online       float64 brute force; within 1e-6 of decode.
-  partials / merge    merge(partials(S)) == decode for S in {1,2,7,64}; empty splits
-                      are exactly (m=-3e38, l=0); an all-empty merge is NaN as in
+  partials / merge    merge(partials(S)) == decode for S in {1,2,7,64}; each partition's
+                      (m, l, acc) against float64 brute force over exactly its tokens
+                      (m = the maximum scaled score); empty splits are exactly
+                      (m=-3e38, l=0); an all-empty merge is NaN as in
                       kernels/paged_attn_v3.cu:162.
   partition_bounds    tiling invariants over a grid of (ctx, S) plus known answers.
   choose_num_splits   the 9 split counts printed in the reference's results
@@ -250,6 +252,31 @@ def test_merge_of_partials_equals_decode(S):
             if en <= st:
                 assert np.all(m[b, :, s] == np.float32(-3e38)) and np.all(l[b, :, s] == 0)
                 assert np.all(acc[b, :, s] == 0)
+
+
+@pytest.mark.parametrize("S", [2, 7, 64])
+def test_partials_vs_float64_brute_force(S):
+    """Each non-empty partition's state, directly: m is the maximum of the
+    scaled scores over exactly the partition's tokens, l = sum exp(s - m),
+    acc = sum exp(s - m) v (kernels/paged_attn_v3.cu:86-122), in float64."""
+    inp = oracle.paged_inputs(3, 4, 2, 32, 16, [1, 77, 300], seed=10 + S, kv_dtype="f16")
+    scale = 0.2
+    acc, m, l = oracle.decode_partials(inp["q_f32"], inp["k"], inp["v"], inp["bt"], inp["ctx"], scale, S, "f16")
+    q = inp["q_f32"].astype(np.float64)
+    G = 4 // 2
+    for b, n in enumerate(inp["ctx"]):
+        K, V = gathered(inp, "f16", b, int(n))
+        for h in range(4):
+            sc = K[h // G] @ q[b, h] * scale
+            for s in range(S):
+                st, en = oracle.partition_bounds(int(n), S, s)
+                if en <= st:
+                    continue
+                mm = sc[st:en].max()
+                w = np.exp(sc[st:en] - mm)
+                np.testing.assert_allclose(m[b, h, s], mm, rtol=1e-6, atol=1e-6)
+                np.testing.assert_allclose(l[b, h, s], w.sum(), rtol=1e-5)
+                np.testing.assert_allclose(acc[b, h, s], w @ V[h // G][st:en], rtol=1e-4, atol=1e-5)
 
 
 def test_all_empty_merge_is_nan_like_reference():
