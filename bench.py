@@ -760,6 +760,14 @@ def make_c2(pa, pools):
                           pools=pools, seed=2, name="decode_c2")
 
 
+def make_c2_fp32io(pa, pools):
+    """Config 2 with the reference's operator dtypes: fp32 q and fp32 out over
+    the fp16 cache (kernels/paged_attn_v3.cu:40,130,220-221)."""
+    return DecodeWorkload(pa, B=64, H=12, HKV=12, D=64, BS=16, ctx=[2048] * 64, dtype=torch.float16,
+                          pools=pools, seed=2, name="decode_c2_fp32io", q_dtype=torch.float32,
+                          out_dtype=torch.float32)
+
+
 def make_c2_fp8(pa, pools):
     """Config 2's geometry over an FP8 E4M3 cache (per-tensor scale 1/16)."""
     return DecodeWorkload(pa, B=64, H=12, HKV=12, D=64, BS=16, ctx=[2048] * 64, dtype=torch.float8_e4m3fn,
@@ -980,7 +988,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--pools", type=int, default=6, help="rotated KV pools (config 2)")
     ap.add_argument("--workload", default="decode_c2",
-                    choices=["decode_c2", "decode_c3", "decode_c5", "decode_c2_fp8", "decode_c3_fp8", "decode_gqa8",
+                    choices=["decode_c2", "decode_c2_fp32io", "decode_c3", "decode_c5", "decode_c2_fp8", "decode_c3_fp8", "decode_gqa8",
                              "decode_c2_split", "sweep", "prefill_c4a", "prefill_c4b", "prefill_ref_chunk",
                              "write_kv_c4a", "write_kv_c4b", "call_overhead", "mixed_c2", "copy_calib"],
                     help="with --only: run just this workload's kernel loop (for profiling)")
@@ -1029,6 +1037,7 @@ def main():
             print(json.dumps(write_record(work, args.steps, args.warmup)), flush=True)
         else:
             work = {"decode_c2": lambda: make_c2(pa, args.pools), "decode_c3": lambda: make_c3(pa, 2),
+                    "decode_c2_fp32io": lambda: make_c2_fp32io(pa, args.pools),
                     "decode_c2_fp8": lambda: make_c2_fp8(pa, args.pools),
                     "decode_c3_fp8": lambda: make_c3_fp8(pa, 2),
                     "decode_gqa8": lambda: make_gqa8(pa, 2),
@@ -1089,7 +1098,8 @@ def main():
     if not args.no_also:
         log("bench: config 2 through the explicit split + LSE reduce")
         also += c2_split_records(pa, args.pools, max(20, args.steps // 4))
-        for make in (lambda: make_c3(pa, 2), lambda: make_c5(pa), lambda: make_c2_fp8(pa, args.pools),
+        for make in (lambda: make_c2_fp32io(pa, args.pools), lambda: make_c3(pa, 2), lambda: make_c5(pa),
+                     lambda: make_c2_fp8(pa, args.pools),
                      lambda: make_c3_fp8(pa, 2), lambda: make_gqa8(pa, 2)):
             w = make()
             log(f"bench: {w.name}")

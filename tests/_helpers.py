@@ -1,6 +1,9 @@
 """Host <-> device plumbing shared by the GPU tests (numpy fixtures -> torch tensors)."""
 from __future__ import annotations
 
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 import torch
 
@@ -39,6 +42,17 @@ def close(got, want, atol=ATOL, rtol=RTOL):
             f"{int(bad.sum())} of {bad.size} outside tol (atol={atol}, rtol={rtol}); first at "
             f"{tuple(i)}: got {got[tuple(i)]} want {want[tuple(i)]}; "
             f"max_abs={np.nanmax(np.abs(got - want)):.3e}")
+
+
+def oracle_decode_rows(q, k, v, bt, ctx, scale, kv, rows_per_call=8):
+    """oracle.decode over the rows of q (axis 0) in parallel threads (the C oracle
+    runs without the interpreter lock), for full-size checks."""
+    n = q.shape[0]
+    chunks = [slice(i, min(n, i + rows_per_call)) for i in range(0, n, rows_per_call)]
+    workers = max(1, min(16, os.cpu_count() or 1))
+    with ThreadPoolExecutor(workers) as ex:
+        parts = list(ex.map(lambda s: oracle.decode(q[s], k, v, bt[s], ctx[s], scale, kv), chunks))
+    return np.concatenate(parts, axis=0)
 
 
 def decode_case(B, H, HKV, D, BS, ctx, *, seed, kv="f16", q="f32", extra_blocks=0, mb=None):

@@ -8,11 +8,12 @@ and check what the oracle can afford there:
     for the library's split plan and for the reference's split count; block
     permutation invariance bit for bit;
   * config 3 (B=32, 32 query / 8 KV heads, D=128, bf16, ragged contexts in
-    [1024, 32768]): sampled sequences (longest, shortest, two others) against
-    the oracle; block permutation invariance bit for bit;
-  * configs 4a / 4b (causal prefill): sampled query rows against the oracle's
-    decode of the row's prefix (a prefill row is the decode of its prefix,
-    which tests/test_oracle.py pins);
+    [1024, 32768]): every sequence against the oracle; block permutation
+    invariance bit for bit;
+  * configs 4a / 4b (causal prefill): query rows against the oracle's decode
+    of the row's prefix (a prefill row is the decode of its prefix, which
+    tests/test_oracle.py pins) -- every row of 4a, and at 4b every 16th row
+    plus the rows on each side of every 128-row work-group boundary;
   * config 5 (layer 11 of a [12, 2, 131072, 16, 12, 64] fp16 pool, 77 GB,
     K base 35.4 G elements in): the layer read in place against a copy of
     it, bit for bit, and sampled sequences against the oracle;
@@ -28,7 +29,7 @@ import pytest
 import torch
 
 import oracle
-from _helpers import close, to_host
+from _helpers import close, oracle_decode_rows, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -107,18 +108,18 @@ def test_config3_full(pa, dev):
     cl = torch.from_numpy(ctx).to(dev)
     scale = 1.0 / np.sqrt(D)
     got = pa.paged_attention_v3(q, k, v, bt, cl, scale, 0, out_dtype=torch.float32)
-    sel = [int(np.argmax(ctx)), int(np.argmin(ctx)), 5, 17]
-    want = oracle.decode(q[sel].float().cpu().numpy(), host_kv(k), host_kv(v), bt_np[sel], ctx[sel], scale, "bf16")
-    close(to_host(got)[sel], want)
+    want = oracle_decode_rows(q.float().cpu().numpy(), host_kv(k), host_kv(v), bt_np, ctx, scale, "bf16", 1)
+    close(to_host(got), want)
     got16 = pa.paged_attention_v3(q, k, v, bt, cl, scale, 0, out_dtype=torch.bfloat16)
     k2, v2, bt2 = permuted(k, v, bt, 33)
     got2 = pa.paged_attention_v3(q, k2, v2, bt2, cl, scale, 0, out_dtype=torch.bfloat16)
     assert torch.equal(got16, got2), "block permutation changed the output"
 
 
-PREFILL = {  # name: (B, S, H, D, dtype, rows sampled)
-    "4a": (8, 1024, 12, 64, torch.float16, [0, 1, 2, 63, 64, 127, 128, 129, 511, 777, 1022, 1023]),
-    "4b": (2, 4096, 32, 128, torch.bfloat16, [0, 1, 63, 64, 127, 128, 129, 1000, 2047, 2048, 4094, 4095]),
+PREFILL = {  # name: (B, S, H, D, dtype, rows checked)
+    "4a": (8, 1024, 12, 64, torch.float16, list(range(1024))),
+    "4b": (2, 4096, 32, 128, torch.bfloat16,
+           sorted(set(range(0, 4096, 16)) | {r + d for r in range(128, 4096, 128) for d in (-1, 0)} | {1, 4095})),
 }
 
 
@@ -141,7 +142,7 @@ def test_prefill_config_full(pa, dev, name):
     bs = [b for b in range(B) for _ in rows]
     rs = [r for _ in range(B) for r in rows]
     qd = q.float().cpu().numpy()[bs, rs]                    # [N, H, D]
-    want = oracle.decode(qd, host_kv(k), host_kv(v), bt_np[bs], np.asarray(rs, np.int32) + 1, scale, kv_tag(dt))
+    want = oracle_decode_rows(qd, host_kv(k), host_kv(v), bt_np[bs], np.asarray(rs, np.int32) + 1, scale, kv_tag(dt))
     close(got[bs, rs], want)
 
 
