@@ -159,6 +159,26 @@ def test_mfma_prefill_bf16_values_beyond_fp16(pa, dev, D):
     close(to_host(got), want)
 
 
+@pytest.mark.parametrize("kv,D", [("f16", 64), ("f16", 128), ("bf16", 64)])
+def test_mfma_prefill_score_jumps(pa, dev, kv, D):
+    """Scores that jump far above every earlier key's: the chunk's first page
+    of K rows scaled by 1/40, a middle page's by 40 (scores spread over ~40 in
+    natural units), so the running maximum moves by far more than the lazy
+    rescale's 2^8 on a late tile; the rows that see the large keys and those
+    that do not must both match the oracle."""
+    S, BS = 300, 16
+    inp = prefill_case(2, S, 4, 2, D, BS, [S, S + 50], seed=D + 5, kv=kv, qt=kv)
+    k = oracle.to_float(inp["k"], kv).copy()
+    for b in range(2):
+        off = inp["ctx"][b] - S
+        for key, f in [(off + j, 1.0 / 40) for j in range(BS)] + [(off + 150 + j, 40.0) for j in range(BS)]:
+            k[inp["bt"][b, key // BS], key % BS] *= f
+    inp["k"] = oracle.quantize(k, kv)
+    scale = 1.0 / np.sqrt(D)
+    got = pa.paged_attention_prefill_wmma(*dev_args(inp, dev), scale)
+    close(to_host(got), want_of(inp, scale))
+
+
 @pytest.mark.parametrize("scale", [-0.15, 0.0])
 @pytest.mark.parametrize("kv,qt", [("f16", "f16"), ("bf16", "bf16"), ("f16", "f32")])
 def test_mfma_prefill_scale_sign(pa, dev, scale, kv, qt):
