@@ -77,9 +77,10 @@ constexpr int kDecodeWaves = PA_DECODE_WAVES;
 constexpr int kDecodeThreads = 64 * kDecodeWaves;
 constexpr int kBtChunk = 256;  // block-table entries staged in LDS at a time
 
-// HP > 1 (MHA only, GC = 1): one work-group serves HP adjacent KV heads,
-// whose rows of a token are contiguous in the pool, as one row of HP * D
-// elements (up to 512 bytes).  A head's row shorter than a 128-byte line
+// HP > 1 (MHA, or GQA groups of four): one work-group serves HP adjacent KV
+// heads, whose rows of a token are contiguous in the pool, as one row of
+// HP * D elements (up to 512 bytes); with GC > 1 the lanes of each head's
+// part of the row serve that KV head's GC query heads.  A head's row shorter than a 128-byte line
 // (FP8 at D = 64, 16-bit at D = 32) then costs whole-line requests instead of
 // half-line ones, and longer packed rows keep more of each DRAM access
 // useful; each head keeps its own softmax (the dot product is summed over
@@ -96,17 +97,16 @@ constexpr int kBtChunk = 256;  // block-table entries staged in LDS at a time
 template <typename KV, int D, int GC, int HP = 1, int DQ = 0>
 __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(GC <= 4 ? 2 : 1)))
 void decode_kernel(const DecodeParams p) {
-  static_assert(HP == 1 || GC == 1, "head pairing serves MHA groups");
   static_assert(DQ == 0 || (pair_types<KV>::value & (1 << DQ)), "the cache cannot provide q's pairs");
   constexpr bool LAZY = PA_DECODE_LAZY && GC >= 2;
   using Sh = DecodeShape<KV, D * HP, (GC == 1 && HP == 1) ? PA_DECODE_NI_MHA : 0>;
   constexpr int VEC = Sh::VEC, LPT = Sh::LPT, TPI = Sh::TPI, NI = Sh::NI, TT = Sh::TT;
   // Packed P.V for GQA groups over fp16 or FP8 caches (V as fp16 pairs);
   // bf16 weights would be too coarse, so bf16 caches keep the fp32 path.
-  // Groups of four heads whose token row spans one 16-lane DPP row: each lane
-  // of a quad finishes one head's score (transposing reduction) and its
+  // Groups of four heads whose KV head's row spans one 16-lane DPP row: each
+  // lane of a quad finishes one head's score (transposing reduction) and its
   // exponential, shared across the quad.
-  constexpr bool PBC = PA_DECODE_PBCAST && LAZY && GC == 4 && LPT == 16;
+  constexpr bool PBC = PA_DECODE_PBCAST && LAZY && GC == 4 && D / VEC == 16;
   constexpr bool PVP = PA_DECODE_PVDOT && LAZY && (Sh::NI % 2 == 0) && KV::kCode != kBF16 &&
                        ((pair_types<KV>::value >> kF16) & 1);
   constexpr int LPH = D / VEC;  // lanes per head's row
@@ -647,6 +647,15 @@ hipError_t launch_decode_d(const DecodeParams& p, int gc, hipStream_t stream) {
     }
     if constexpr (D * KV::kBytes * 2 <= PA_PACK_ROW_BYTES) {
       if (p.hp == 2) return launch_decode_dg<KV, D, 1, 2>(p, stream);
+    }
+  }
+  // GQA groups of four with two (or four) KV heads per work-group (one head chunk).
+  if (gc == 4 && p.G == 4 && p.hp > 1 && p.k_sh == D && p.v_sh == D && p.HKV % p.hp == 0) {
+    if constexpr (KV::kBytes == 2 && D * KV::kBytes * 4 <= PA_PACK_GQA_ROW_BYTES && PA_PACK_GQA_MAX >= 4) {
+      if (p.hp == 4) return launch_decode_dg<KV, D, 4, 4>(p, stream);
+    }
+    if constexpr (KV::kBytes == 2 && D * KV::kBytes * 2 <= PA_PACK_GQA_ROW_BYTES && PA_PACK_GQA_MAX >= 2) {
+      if (p.hp == 2) return launch_decode_dg<KV, D, 4, 2>(p, stream);
     }
   }
   switch (gc) {

@@ -618,3 +618,31 @@ def test_unattended_slots_hold_nan(pa, dev, kind, H, HKV, D, BS):
         got = to_host(pa.paged_attention_prefill_wmma(qpd, kd, vd, btd, ctxd, scale))
         assert np.isfinite(got).all()
         close(got, wantp)
+
+
+@pytest.mark.parametrize("kind,D,qt", [("bf16", 128, "bf16"), ("f16", 128, "f16"), ("bf16", 64, "bf16"),
+                                       ("f16", 128, "f32")])
+def test_gqa4_two_kv_heads_per_work_group(pa, dev, kind, D, qt):
+    """GQA groups of four over 16-bit caches whose heads are contiguous: a
+    grid that fills the GPU serves two KV heads per work-group (one 2*D-element
+    row per token, each lane computing its own KV head's four query heads).
+    Ragged contexts with NaN and Inf planted in every unattended slot; the
+    explicit split must dispatch the two-head kernel and match the oracle, as
+    must the library's own plan."""
+    B, H, HKV, BS = 64, 16, 4, 16
+    ctx = np.random.default_rng(D + 5).integers(1, 700, B).astype(np.int32)
+    inp = decode_case(B, H, HKV, D, BS, ctx, seed=D + 9, kv=kind, q=qt, extra_blocks=1)
+    k, v, bt = _poison_unattended(inp["k"], inp["v"], inp["bt"], inp["ctx"], BS, kind)
+    kd, vd = to_dev(k, kind, dev), to_dev(v, kind, dev)
+    q = to_dev(inp["q"], inp["qt"], dev)
+    btd, ctxd = torch.from_numpy(bt).to(dev), torch.from_numpy(inp["ctx"]).to(dev)
+    scale = 1.0 / np.sqrt(D)
+    want = oracle.decode(inp["q_f32"], k, v, bt, inp["ctx"], scale, kind)
+    assert np.isfinite(want).all()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    for ns in (8, 0):
+        got = to_host(pa.paged_attention_v3(q, kd, vd, btd, ctxd, scale, ns, out_dtype=torch.float32))
+        if ns and B * (HKV // 2) * ns >= 3 * cus:
+            assert f"{D}, 4, 2, " in pa.last_launch(), pa.last_launch()
+        assert np.isfinite(got).all(), ns
+        close(got, want)
