@@ -154,12 +154,12 @@ hipError_t launch_write_kv(const WriteParams& p, hipStream_t stream);
 #endif
 
 // Widest packing the layout allows (1 = none).  GQA groups of four query
-// heads over 16-bit caches pack too: each lane still serves one KV head's
+// heads over 8/16-bit caches pack too: each lane still serves one KV head's
 // group, so the vector work per lane is unchanged and only the rows read
-// together get wider (config 3, two KV heads: 5819 -> 5968 GB/s).  (FP8
-// groups of four would lose an occupancy step: 4443 -> 4197.)
+// together get wider (two KV heads: config 3 5819 -> 5968 GB/s, FP8 config 3
+// 4550 -> 4753).
 inline int decode_pack_max(int D, int kv_bytes, int G, int HKV, int64_t k_sh) {
-  if (k_sh != D || !(G == 1 || (G == 4 && kv_bytes == 2))) return 1;
+  if (k_sh != D || !(G == 1 || (G == 4 && kv_bytes <= 2))) return 1;
   const int most = G == 1 ? PA_PACK_MAX : PA_PACK_GQA_MAX;
   const int64_t row = G == 1 ? PA_PACK_ROW_BYTES : PA_PACK_GQA_ROW_BYTES;
   int hp = 1;

@@ -88,6 +88,18 @@ constexpr int kBtChunk = 256;  // block-table entries staged in LDS at a time
 // Groups of up to 4 heads are held to two waves per SIMD (<= 256 registers),
 // which the loads in flight need; left to itself the allocator has tipped
 // GC = 4 at D = 128 into one wave per SIMD (config 3: 415 -> 518 us).
+// Register budget (waves per SIMD the allocator must fit): groups of up to 4
+// heads two (above); the FP8 group of four at D = 128 packed two KV heads
+// to a work-group three, which it fits with one spilled register outside
+// the loop (170 registers otherwise: FP8 config 3 4550 -> 4753 GB/s); larger
+// groups one.
+template <typename KV, int D, int GC, int HP, int DQ>
+constexpr int decode_waves_per_eu() {
+  if (GC > 4) return 1;
+  if (KV::kCode == kFP8 && GC == 4 && HP == 2 && D == 128 && DQ != 0) return 3;
+  return 2;
+}
+
 // DQ (kF16 or kBF16): q is fp16 or bf16 and the cache provides element pairs
 // of that type (the raw words of a cache of q's dtype; FP8 codes through one
 // packed conversion per pair), so q is held as packed pairs (exact) and each
@@ -95,7 +107,7 @@ constexpr int kBtChunk = 256;  // block-table entries staged in LDS at a time
 // instead of widening K to fp32 and VEC fused multiply-adds: the score costs
 // a quarter of the vector instructions (GQA groups are bound by them).
 template <typename KV, int D, int GC, int HP = 1, int DQ = 0>
-__global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(GC <= 4 ? 2 : 1)))
+__global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<KV, D, GC, HP, DQ>())))
 void decode_kernel(const DecodeParams p) {
   static_assert(DQ == 0 || (pair_types<KV>::value & (1 << DQ)), "the cache cannot provide q's pairs");
   constexpr bool LAZY = PA_DECODE_LAZY && GC >= 2;
@@ -654,7 +666,7 @@ hipError_t launch_decode_d(const DecodeParams& p, int gc, hipStream_t stream) {
     if constexpr (KV::kBytes == 2 && D * KV::kBytes * 4 <= PA_PACK_GQA_ROW_BYTES && PA_PACK_GQA_MAX >= 4) {
       if (p.hp == 4) return launch_decode_dg<KV, D, 4, 4>(p, stream);
     }
-    if constexpr (KV::kBytes == 2 && D * KV::kBytes * 2 <= PA_PACK_GQA_ROW_BYTES && PA_PACK_GQA_MAX >= 2) {
+    if constexpr (KV::kBytes <= 2 && D * KV::kBytes * 2 <= PA_PACK_GQA_ROW_BYTES && PA_PACK_GQA_MAX >= 2) {
       if (p.hp == 2) return launch_decode_dg<KV, D, 4, 2>(p, stream);
     }
   }

@@ -646,3 +646,29 @@ def test_gqa4_two_kv_heads_per_work_group(pa, dev, kind, D, qt):
             assert f"{D}, 4, 2, " in pa.last_launch(), pa.last_launch()
         assert np.isfinite(got).all(), ns
         close(got, want)
+
+
+@pytest.mark.parametrize("D,qt", [(128, torch.bfloat16), (128, torch.float32), (64, torch.float16)])
+def test_fp8_gqa4_two_kv_heads_per_work_group(pa, dev, D, qt):
+    """The FP8 group of four with two KV heads per work-group (the kernel held
+    to three waves per SIMD for 16-bit q at D = 128): ragged contexts, NaN
+    planted in every unattended slot, scaled cache, against the oracle."""
+    B, H, HKV, BS = 64, 16, 4, 16
+    ctx = np.random.default_rng(D + 11).integers(1, 700, B).astype(np.int32)
+    inp, k8, v8, _, _ = fp8_case(B, H, HKV, D, BS, ctx, seed=D + 13, k_scale=0.05, v_scale=0.02)
+    k8, v8 = np.concatenate([k8, k8[:1]]), np.concatenate([v8, v8[:1]])  # a spare block
+    k8, v8, bt = _poison_unattended(k8, v8, inp["bt"], inp["ctx"], BS, "fp8")
+    kf, vf = oracle.fp8_decode(k8) * np.float32(0.05), oracle.fp8_decode(v8) * np.float32(0.02)
+    q = torch.from_numpy(inp["q_f32"]).to(dev).to(qt)
+    qf = q.float().cpu().numpy()  # q as the kernel sees it
+    btd, ctxd = torch.from_numpy(bt).to(dev), torch.from_numpy(inp["ctx"]).to(dev)
+    want = oracle.decode(qf, kf, vf, bt, inp["ctx"], 0.1, "f32")
+    assert np.isfinite(want).all()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    for ns in (8, 0):
+        got = to_host(pa.paged_attention_v3(q, fp8_dev(k8, dev), fp8_dev(v8, dev), btd, ctxd, 0.1, ns,
+                                            k_scale=0.05, v_scale=0.02))
+        if ns and B * (HKV // 2) * ns >= 3 * cus:
+            assert f"{D}, 4, 2, " in pa.last_launch(), pa.last_launch()
+        assert np.isfinite(got).all(), ns
+        close(got, want)
