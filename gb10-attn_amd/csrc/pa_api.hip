@@ -492,8 +492,8 @@ int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const p
 // MFMA prefill launch for checked arguments; cu != null selects the
 // variable-length layout (rows cu[b] .. cu[b+1] of a packed [T, H, D] q/out).
 int run_prefill_mfma(DecodeArgs& a, const pa_tensor_t* q, const int32_t* cu, int64_t T, double scale,
-                     void* stream) {
-  g_launches.clear();
+                     void* stream, bool route_single = false) {
+  if (!route_single) g_launches.clear();
   // kernels/paged_attn_wmma.cu:220-223 requires fp16; bf16 is served as well.
   if (a.kv_dtype != kF16 && a.kv_dtype != kBF16)
     return fail(PA_ERR_INVALID_ARGUMENT, "the MFMA path needs an fp16 or bf16 KV cache");
@@ -515,6 +515,7 @@ int run_prefill_mfma(DecodeArgs& a, const pa_tensor_t* q, const int32_t* cu, int
   pp.bs_div = p.bs_div;
   pp.cu_q = cu;
   pp.q_total = T;
+  pp.skip_single = route_single ? 1 : 0;
   // The kernel applies the sign of the scale to q (exactly) and keeps the
   // softmax scale positive, so the running max of raw scores orders as the scaled ones.
   const double log2e = 1.4426950408889634;
@@ -717,7 +718,30 @@ int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const
   rc = check_args(&o4, &q4, k_cache, v_cache, block_tables, context_lens, scale, true, &a);
   if (rc) return rc;
   if (max_q_len == 0 || T == 0) return PA_OK;
-  return run_prefill_mfma(a, q, static_cast<const int32_t*>(cu_seqlens_q->data), T, scale, stream);
+  g_launches.clear();
+  const int32_t* cu = static_cast<const int32_t*>(cu_seqlens_q->data);
+  // Sequences that bring one query row (decode steps of the batch) go to the
+  // decode kernel, one launch over every sequence in which the others' work-
+  // groups exit at once; the prefill kernel then skips them.  The rows are
+  // told apart on the device (cu_seqlens_q is device memory: no host sync).
+  const bool prefill_ok = (a.kv_dtype == kF16 || a.kv_dtype == kBF16) && a.p.D <= 256 &&
+                          (reinterpret_cast<uintptr_t>(q->data) & 15) == 0 && (int64_t)a.p.B * a.p.H > 0;
+  if (prefill_ok) {  // (otherwise the prefill call below reports why, before any launch)
+    DecodeArgs d = a;
+    d.p.Sq = 1;
+    d.p.cu_q = cu;
+    d.p.q_total = T;
+    d.p.parts = 1;
+    d.p.part_tokens = 0;
+    d.p.direct = 1;
+    int cus = 0;
+    if ((rc = device_cu_count(&cus))) return rc;
+    d.p.hp = pack_for(d.p, dtype_bytes(d.kv_dtype), 1, cus);
+    if ((rc = hip_status(launch_decode(d.p, d.kv_dtype, d.gc, static_cast<hipStream_t>(stream)),
+                         "decode kernel launch")))
+      return rc;
+  }
+  return run_prefill_mfma(a, q, cu, T, scale, stream, true);
 }
 
 int pa_write_kv(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tensor_t* key,

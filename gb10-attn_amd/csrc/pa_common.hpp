@@ -63,6 +63,10 @@ struct DecodeParams {
   FastDiv bs_div;
   float qscale;         // scale * k_scale * log2(e): scores come out in log2 units
   float vscale;         // v_scale (FP8 caches): applied to the weighted V sum
+  // Variable-length batches (Sq = 1): [B + 1] row offsets into packed [T, H, D]
+  // q/out; only sequences of exactly one row are served (else null).
+  const int32_t* cu_q;
+  int64_t q_total;
 };
 
 struct ReduceParams {
@@ -94,6 +98,7 @@ struct PrefillParams {
   int32_t wg_cus;    // > 0: the whole grid is resident on this many CUs (work-group order)
   const int32_t* cu_q;  // variable-length batches: [B + 1] row offsets into [T, H, D] q/out (else null)
   int64_t q_total;      // T (variable-length batches)
+  int32_t skip_single;  // variable-length batches: sequences of one row are served by the decode kernel
   int32_t q_split;   // q is not exactly the KV type: add a low-part product
   FastDiv bs_div;
   float qscale;      // |scale| * log2(e), or 1 when scale == 0 (always positive)

@@ -158,6 +158,14 @@ void decode_kernel(const DecodeParams p) {
   const int b = z / p.Sq;
   const int sq = z - b * p.Sq;
   const int g0 = hc * GC;
+  // q/out row: z, or in a variable-length batch the packed row of a sequence
+  // that brings exactly one query row (others are the prefill kernel's).
+  int64_t zq = z;
+  if (p.cu_q) {
+    const int qa = p.cu_q[b], qe = p.cu_q[b + 1];
+    if (!(qa >= 0 && qe == qa + 1 && (int64_t)qe <= p.q_total)) return;  // work-group uniform
+    zq = qa;
+  }
 
   const int maxctx = p.MB * p.BS;
   const int ctx_b = p.context_lens[b];
@@ -176,7 +184,7 @@ void decode_kernel(const DecodeParams p) {
         const int d = dd % D, hh = dd / D;
         if (g0 + g >= p.G) continue;
         const int h = (kvh * HP + hh) * p.G + g0 + g;
-        store_elem(p.out, p.out_dtype, ((int64_t)z * p.H + h) * D + d, fillv);
+        store_elem(p.out, p.out_dtype, (zq * p.H + h) * D + d, fillv);
       }
     }
     return;
@@ -199,7 +207,7 @@ void decode_kernel(const DecodeParams p) {
   for (int g = 0; g < GC; ++g) {
     const bool hv = g0 + g < p.G;
     const int h = (kvh * HP + hl) * p.G + g0 + (hv ? g : 0);
-    const int64_t qb = ((int64_t)z * p.H + h) * D + dsub * VEC;
+    const int64_t qb = (zq * p.H + h) * D + dsub * VEC;
     load_elems<VEC>(p.q, p.q_dtype, qb, qr[g]);
   }
 #pragma unroll
@@ -611,7 +619,7 @@ void decode_kernel(const DecodeParams p) {
     }
     const int h = (kvh * HP + hh) * p.G + g0 + g;
     if (final_here) {
-      store_elem(p.out, p.out_dtype, ((int64_t)z * p.H + h) * D + d,
+      store_elem(p.out, p.out_dtype, (zq * p.H + h) * D + d,
                  bad ? __builtin_nanf("") : A * p.vscale / L);
     } else {
       const int64_t pidx = ((int64_t)b * p.H + h) * p.parts + part;

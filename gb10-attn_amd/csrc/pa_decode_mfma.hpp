@@ -440,7 +440,7 @@ bool decode_mfma_eligible(const DecodeParams& p, int gc) {
     return false;
   } else {
     const bool aligned = p.part_tokens > 0 ? p.part_tokens % 16 == 0 : p.parts == 1;
-    return gc >= 8 && p.Sq == 1 && p.BS % 16 == 0 && aligned && PA_DECODE_MFMA;
+    return gc >= 8 && p.Sq == 1 && p.BS % 16 == 0 && aligned && !p.cu_q && PA_DECODE_MFMA;
   }
 }
 

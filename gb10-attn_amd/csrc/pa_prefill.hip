@@ -253,6 +253,7 @@ void prefill_mfma_kernel(const PrefillParams p) {
     const bool ok = qa >= 0 && qb >= qa && (int64_t)qb <= p.q_total;
     S = ok ? qb - qa : 0;
     tok0 = ok ? qa : 0;
+    if (p.skip_single && S == 1) return;  // the decode kernel serves it (work-group uniform)
   }
   const int Sr = min(S, p.S);
   const int ctx = p.context_lens[b];

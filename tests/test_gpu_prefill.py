@@ -203,7 +203,8 @@ def varlen_case(qlens, ctxs, H, HKV, D, BS, seed, kv, qt="f32"):
 def test_varlen_mixed_decode_and_prefill(pa, dev, kv, D):
     """Sequences bringing 1 (decode), 0, 37, 130 and 300 new tokens against
     contexts of equal or larger length (chunked): each sequence's rows equal
-    the oracle's prefill of that sequence alone; decode rows equal decode."""
+    the oracle's prefill of that sequence alone; decode rows (served by the
+    decode kernel in the same call) equal decode."""
     qlens = [1, 37, 0, 130, 1, 300]
     ctxs = [700, 37, 20, 1000, 1, 333]
     H, HKV, BS = 4, 2, 16
@@ -212,6 +213,9 @@ def test_varlen_mixed_decode_and_prefill(pa, dev, kv, D):
         to_dev(q, kv, dev), to_dev(inp["k"], kv, dev), to_dev(inp["v"], kv, dev),
         torch.from_numpy(inp["bt"]).to(dev), torch.from_numpy(inp["ctx"]).to(dev),
         torch.from_numpy(cu).to(dev), max(qlens), 1.0 / np.sqrt(D)))
+    # The one-row sequences went to the decode kernel, the others to the prefill kernel.
+    launched = pa.last_launch()
+    assert "decode_kernel" in launched and "prefill_mfma_kernel" in launched, launched
     for b, n in enumerate(qlens):
         if n == 0:
             continue
@@ -251,6 +255,32 @@ def test_varlen_malformed_ranges_and_max_q_len(pa, dev):
             want = oracle.prefill(q32[5:45][None], inp["k"], inp["v"], inp["bt"][1:2], inp["ctx"][1:2],
                                   0.125, "f16")[0]
             close(got[5:5 + 32], want[:32])
+
+
+@pytest.mark.parametrize("kv,D", [("f16", 64), ("bf16", 128)])
+def test_varlen_all_single_rows(pa, dev, kv, D):
+    """A batch of decode steps (max_q_len = 1), served by the decode kernel in
+    the varlen call: sequences of one row match the oracle's decode, one with
+    an empty context is zeros, and a sequence without rows writes nothing."""
+    qlens = [1, 1, 0, 1, 1]
+    ctxs = [300, 17, 40, 1, 900]
+    H, HKV, BS = 8, 2, 16
+    inp, q, q32, cu = varlen_case(qlens, ctxs, H, HKV, D, BS, seed=D + 2, kv=kv, qt=kv)
+    ctx = inp["ctx"].copy()
+    ctx[3] = 0
+    T = int(cu[-1])
+    out = torch.full((T, H, D), 7.0, device=dev)
+    pa.paged_attention_prefill_varlen(to_dev(q, kv, dev), to_dev(inp["k"], kv, dev), to_dev(inp["v"], kv, dev),
+                                      torch.from_numpy(inp["bt"]).to(dev), torch.from_numpy(ctx).to(dev),
+                                      torch.from_numpy(cu).to(dev), 1, 1.0 / np.sqrt(D), out=out)
+    launched = pa.last_launch()
+    assert "decode_kernel" in launched, launched
+    got = to_host(out)
+    for b in (0, 1, 4):
+        rows = slice(cu[b], cu[b + 1])
+        close(got[rows], oracle.decode(q32[rows], inp["k"], inp["v"], inp["bt"][b:b + 1], ctx[b:b + 1],
+                                       1.0 / np.sqrt(D), kv))
+    assert np.all(got[cu[3]:cu[4]] == 0.0)
 
 
 @pytest.mark.parametrize("kv,qt", [("f16", "f16"), ("bf16", "bf16"), ("f16", "f32"), ("bf16", "f32")])
