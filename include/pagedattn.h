@@ -223,7 +223,10 @@ int paged_attention_v3_noalloc(pa_tensor_t* out, const pa_tensor_t* q, const pa_
  * paged_attention_prefill_wmma.  cu_seqlens_q is int32 [B + 1] on the device;
  * max_q_len must bound every q_len_b (rows past it are not written).  A
  * sequence whose range is negative, decreasing or beyond T is skipped (its
- * rows are not written); nothing is read out of bounds. */
+ * rows are not written); nothing is read out of bounds.  Sequences of one
+ * row are computed by the decode kernel and the others by the MFMA prefill
+ * kernel: two launches on the stream, told apart on the device (no host
+ * synchronisation). */
 int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
                                    const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
                                    const pa_tensor_t* context_lens, const pa_tensor_t* cu_seqlens_q,
