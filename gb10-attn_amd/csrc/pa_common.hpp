@@ -60,6 +60,7 @@ struct DecodeParams {
   int32_t part_tokens;  // > 0: fixed partition length; 0: chunk = ceil(ctx / parts)
   int32_t direct;       // 1: one partition, every WG writes the normalised output
   int32_t hp;           // KV heads per work-group (head packing: MHA, or GQA groups of four); <= 1: one
+  int32_t pprio;        // 1: the whole grid is resident at once; waves lower their priority as they progress
   FastDiv bs_div;
   float qscale;         // scale * k_scale * log2(e): scores come out in log2 units
   float vscale;         // v_scale (FP8 caches): applied to the weighted V sum
