@@ -302,9 +302,17 @@ def check_write(work):
     t = torch.tensor(sorted({0, 1, T // 3, T // 2, T - 2, T - 1}), device=key.device)
     sl = slots[t].long()
     blk, row = sl // work.BS, sl % work.BS
-    ok = bool(torch.equal(kc[blk, row], key[t]) and torch.equal(vc[blk, row], val[t]))
-    return {"what": f"{t.numel()} tokens' K/V rows at their slots vs the source rows, bit for bit",
-            "ok": ok}, kernels
+    if work.cache_dtype == work.dtype and work.kv_scale == 1.0:
+        ok = bool(torch.equal(kc[blk, row], key[t]) and torch.equal(vc[blk, row], val[t]))
+        what = f"{t.numel()} tokens' K/V rows at their slots vs the source rows, bit for bit"
+    else:  # torch's own cast of source / scale (no value here reaches the FP8 saturation range)
+        sc = torch.tensor(work.kv_scale, dtype=torch.float32, device=key.device)
+        wk = (key[t].float() / sc).to(work.cache_dtype)
+        wv = (val[t].float() / sc).to(work.cache_dtype)
+        as_bits = (lambda x: x.view(torch.uint8)) if work.cache_dtype == torch.float8_e4m3fn else (lambda x: x)
+        ok = bool(torch.equal(as_bits(kc[blk, row]), as_bits(wk)) and torch.equal(as_bits(vc[blk, row]), as_bits(wv)))
+        what = f"{t.numel()} tokens' K/V rows at their slots vs torch's cast of source / scale, bit for bit"
+    return {"what": what, "ok": ok}, kernels
 
 
 def check_mixed(w):
@@ -347,8 +355,10 @@ class WriteWorkload:
     block table's slots (pa_write_kv), rotated over `copies` disjoint
     (source, pool) pairs so each step reads and writes HBM, not cache."""
 
-    def __init__(self, pa, *, B, S, HKV, D, BS, dtype, seed, name, copies=8):
+    def __init__(self, pa, *, B, S, HKV, D, BS, dtype, seed, name, copies=8, cache_dtype=None, kv_scale=1.0):
         self.pa, self.name, self.dtype, self.BS = pa, name, dtype, BS
+        self.cache_dtype = cache_dtype or dtype
+        self.kv_scale = kv_scale  # the cache holds key / kv_scale and value / kv_scale
         dev = torch.device("cuda:0")
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
@@ -363,17 +373,19 @@ class WriteWorkload:
             slots = torch.from_numpy((perm[:, tok // BS] * BS + tok % BS).reshape(-1)).to(dev)
             key = torch.randn((T, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
             val = torch.randn((T, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
-            kc = torch.zeros((nb, BS, HKV, D), device=dev, dtype=dtype)
+            kc = torch.zeros((nb, BS, HKV, D), device=dev, dtype=torch.uint8).view(self.cache_dtype) \
+                if self.cache_dtype == torch.float8_e4m3fn else torch.zeros((nb, BS, HKV, D), device=dev, dtype=dtype)
             vc = torch.zeros_like(kc)
             views = [V(kc), V(vc), V(key), V(val), V(slots)]
             self._keep.append((slots, key, val, kc, vc, views))
             self.args.append([C.byref(x) for x in views])
         es = torch.tensor([], dtype=dtype).element_size()
-        self.bytes = 2.0 * T * HKV * D * 2 * es + T * 8  # K and V read + written, slot mapping
+        ces = torch.tensor([], dtype=self.cache_dtype).element_size()
+        self.bytes = 2.0 * T * HKV * D * (es + ces) + T * 8  # K and V read + written, slot mapping
         self.L = pa.lib()
 
     def launch(self, i, stream, ev_mid=None):
-        rc = self.L.pa_write_kv(*self.args[i % len(self.args)], stream)
+        rc = self.L.pa_write_kv_scaled(*self.args[i % len(self.args)], self.kv_scale, self.kv_scale, stream)
         if rc != 0:
             raise RuntimeError(self.pa.last_error())
 
@@ -391,6 +403,9 @@ PREFILL_CFG = {
 WRITE_CFG = {
     "write_kv_c4a": dict(B=8, S=1024, HKV=12, D=64, dtype=torch.float16, seed=14),
     "write_kv_c4b": dict(B=2, S=4096, HKV=32, D=128, dtype=torch.bfloat16, seed=16),
+    # Config 4b's bf16 prompt quantised into an FP8 E4M3 pool (per-tensor scale 1/16).
+    "write_kv_c4b_fp8": dict(B=2, S=4096, HKV=32, D=128, dtype=torch.bfloat16, seed=16,
+                             cache_dtype=torch.float8_e4m3fn, kv_scale=1.0 / 16),
 }
 
 
@@ -404,6 +419,7 @@ def write_record(work, steps, warmup):
         "workload": work.name, "value": round(gbs, 1), "unit": "GB/s",
         "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4), "ms_per_step": round(ms, 5),
         "kernel_ms": round(kms, 5), "bytes_per_step": work.bytes, "dtype": str(work.dtype).replace("torch.", ""),
+        "cache_dtype": str(work.cache_dtype).replace("torch.", ""),
         "kernels": kernels, "check": chk,
     }
 
@@ -990,7 +1006,7 @@ def main():
     ap.add_argument("--workload", default="decode_c2",
                     choices=["decode_c2", "decode_c2_fp32io", "decode_c3", "decode_c5", "decode_c2_fp8", "decode_c3_fp8", "decode_gqa8",
                              "decode_c2_split", "sweep", "prefill_c4a", "prefill_c4b", "prefill_ref_chunk",
-                             "write_kv_c4a", "write_kv_c4b", "call_overhead", "mixed_c2", "copy_calib"],
+                             "write_kv_c4a", "write_kv_c4b", "write_kv_c4b_fp8", "call_overhead", "mixed_c2", "copy_calib"],
                     help="with --only: run just this workload's kernel loop (for profiling)")
     ap.add_argument("--only", action="store_true", help="time only --workload, print its record")
     ap.add_argument("--no-also", action="store_true", help="skip the secondary configs")

@@ -746,6 +746,12 @@ int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const
 
 int pa_write_kv(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tensor_t* key,
                 const pa_tensor_t* value, const pa_tensor_t* slot_mapping, void* stream) {
+  return pa_write_kv_scaled(k_cache, v_cache, key, value, slot_mapping, 1.0, 1.0, stream);
+}
+
+int pa_write_kv_scaled(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tensor_t* key,
+                       const pa_tensor_t* value, const pa_tensor_t* slot_mapping, double k_scale,
+                       double v_scale, void* stream) {
   g_launches.clear();
   int rc;
   if ((rc = check_tensor(k_cache, "k_cache", 4, "[NB, BS, HKV, D]"))) return rc;
@@ -754,8 +760,11 @@ int pa_write_kv(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tensor_t* k
   if ((rc = check_tensor(value, "value", 3, "[T, HKV, D]"))) return rc;
   if ((rc = check_tensor(slot_mapping, "slot_mapping", 1, "[T]"))) return rc;
   const int cd = k_cache->dtype, sd = key->dtype;
-  if (cd != kF16 && cd != kBF16 && cd != kF32)
-    return fail(PA_ERR_INVALID_ARGUMENT, "k_cache must be float16, bfloat16 or float32 (got %s)", dtype_name(cd));
+  if (cd != kF16 && cd != kBF16 && cd != kF32 && cd != kFP8)
+    return fail(PA_ERR_INVALID_ARGUMENT, "k_cache must be float16, bfloat16, float32 or float8_e4m3fn (got %s)",
+                dtype_name(cd));
+  if (!std::isfinite(k_scale) || !std::isfinite(v_scale) || (float)k_scale == 0.0f || (float)v_scale == 0.0f)
+    return fail(PA_ERR_INVALID_ARGUMENT, "k_scale and v_scale must be finite and nonzero");
   if (v_cache->dtype != cd) return fail(PA_ERR_INVALID_ARGUMENT, "v_cache must have the dtype of k_cache");
   if (sd != kF16 && sd != kBF16 && sd != kF32)
     return fail(PA_ERR_INVALID_ARGUMENT, "key must be float16, bfloat16 or float32 (got %s)", dtype_name(sd));
@@ -813,6 +822,9 @@ int pa_write_kv(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tensor_t* k
   if (T > INT32_MAX) return fail(PA_ERR_UNSUPPORTED, "too many tokens for one call");
   p.HKV = (int32_t)HKV; p.D = (int32_t)D; p.BS = (int32_t)BS;
   p.src_dtype = sd; p.cache_dtype = cd; p.slot_i64 = slot_mapping->dtype == kI64;
+  p.k_scale = (float)k_scale; p.v_scale = (float)v_scale;
+  p.k_rcp = 1.0f / p.k_scale; p.v_rcp = 1.0f / p.v_scale;  // IEEE single division: correctly rounded
+  p.unit_scale = p.k_scale == 1.0f && p.v_scale == 1.0f;
   p.bs_div = make_fastdiv((uint32_t)BS);
   return hip_status(launch_write_kv(p, static_cast<hipStream_t>(stream)), "KV write kernel launch");
 }

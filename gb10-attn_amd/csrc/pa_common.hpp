@@ -122,6 +122,9 @@ struct WriteParams {
   int64_t nslots;      // NB * BS (< 2^31)
   int32_t T, HKV, D, BS;
   int32_t src_dtype, cache_dtype, slot_i64;
+  int32_t unit_scale;  // 1: k_scale == v_scale == 1 (no division)
+  float k_scale, v_scale;  // the cache holds key / k_scale and value / v_scale
+  float k_rcp, v_rcp;      // 1 / k_scale, 1 / v_scale rounded to nearest (fp32)
   FastDiv bs_div;
 };
 

@@ -10,9 +10,12 @@
 // [T, HKV, D] source and slot[t] = block_ids[t / BS] * BS + t % BS.
 //
 // HBM-bound byte work: each thread moves 8 elements of one (token, head) row
-// (one 16-byte store for a 16-bit cache), converting the element type on the
-// way (round to nearest even, as the oracle's codecs).  A negative slot is
-// skipped (padding tokens), as is a slot past the pool; 64-bit offsets.
+// (one 16-byte store for a 16-bit cache, 8 bytes for FP8), converting the
+// element type on the way (round to nearest even, as the oracle's codecs).  A
+// negative slot is skipped (padding tokens), as is a slot past the pool;
+// 64-bit offsets.  With per-tensor scales the cache receives key / k_scale
+// and value / v_scale (fp32 division, correctly rounded), the form the
+// scaled decode entry point reads back.
 #include "pa_device.hpp"
 
 namespace pa {
@@ -44,9 +47,62 @@ __device__ inline void load8(const void* base, int64_t idx, float (&x)[8]) {
   }
 }
 
+// fp32 -> FP8 E4M3 (OCP, "fn": no infinities) code, round to nearest even,
+// saturating at +-448 (the largest finite value; infinities too), NaN ->
+// 0x7f, -0 -> 0x80.  Normal range: the fp32 bits rounded to 3 mantissa bits
+// and rebiased (exponent bias 127 -> 7); below 2^-6 the code is the integer
+// nearest |x| * 2^9 (subnormal steps of 2^-9; 8 is the smallest normal).
+__device__ inline uint32_t fp8_e4m3_code(float x) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, x);
+  const uint32_t sign = (b >> 24) & 0x80u;
+  const uint32_t a = b & 0x7fffffffu;
+  if (a > 0x7f800000u) return 0x7fu;        // NaN
+  if (a >= 0x43e00000u) return sign | 0x7eu;  // |x| >= 448
+  if (a >= 0x3c800000u) {                   // |x| >= 2^-6
+    const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+    return sign | ((r >> 20) - ((127u - 7u) << 3));
+  }
+  return sign | (uint32_t)__builtin_rintf(__builtin_bit_cast(float, a) * 512.0f);
+}
+
+// x / s rounded to nearest, from r = RN(1 / s): q = RN(x r) is within one ulp
+// of x / s, the residual x - q s is exact in one FMA, and RN(q + (x - q s) r)
+// is the correctly rounded quotient (Markstein's theorem) while no
+// intermediate leaves the normal range; outside it (and for zero, NaN,
+// infinities) the full-precision division is taken.
+__device__ inline float div_rn(float x, float s, float r) {
+  const float q = x * r;
+  const float aq = __builtin_fabsf(q);
+  if (!(aq >= 0x1p-100f && aq <= 0x1p100f)) return (x == 0.0f || x != x) ? q : __fdiv_rn(x, s);
+  return __builtin_fmaf(__builtin_fmaf(-q, s, x), r, q);
+}
+
 template <int DST>
 __device__ inline void store8(void* base, int64_t idx, const float (&x)[8]) {
-  if constexpr (DST == kF32) {
+  if constexpr (DST == kFP8) {
+    u32x2_t w;
+    bool nan = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) nan |= x[e] != x[e];
+    if (!nan) {
+      // v_cvt_pk_fp8_f32 (round to nearest even) on values clamped to +-448,
+      // so that every finite or infinite input saturates as fp8_e4m3_code does.
+      float c[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) c[e] = __builtin_fminf(__builtin_fmaxf(x[e], -448.0f), 448.0f);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(c[4 * j], c[4 * j + 1], 0, false);
+        w[j] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c[4 * j + 2], c[4 * j + 3], lo, true);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        w[j] = fp8_e4m3_code(x[4 * j]) | (fp8_e4m3_code(x[4 * j + 1]) << 8) |
+               (fp8_e4m3_code(x[4 * j + 2]) << 16) | (fp8_e4m3_code(x[4 * j + 3]) << 24);
+    }
+    *reinterpret_cast<u32x2_t*>(static_cast<uint8_t*>(base) + idx) = w;
+  } else if constexpr (DST == kF32) {
     float* p = static_cast<float*>(base) + idx;
     *reinterpret_cast<float4_t*>(p) = float4_t{x[0], x[1], x[2], x[3]};
     *reinterpret_cast<float4_t*>(p + 4) = float4_t{x[4], x[5], x[6], x[7]};
@@ -88,18 +144,28 @@ __global__ __launch_bounds__(kWriteThreads) void write_kv_kernel(const WritePara
   const int64_t kd = (int64_t)blk * p.kc_sb + (int64_t)off * p.kc_st + (int64_t)h * p.kc_sh + c * 8;
   const int64_t vd = (int64_t)blk * p.vc_sb + (int64_t)off * p.vc_st + (int64_t)h * p.vc_sh + c * 8;
   if constexpr (SRC == DST && SRC != kF32) {
-    // Same 16-bit type: copy the bits (NaN payloads included).
-    *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(p.kc) + kd) =
-        *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p.key) + ks);
-    *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(p.vc) + vd) =
-        *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p.value) + vs);
-  } else {
-    float x[8];
-    load8<SRC>(p.key, ks, x);
-    store8<DST>(p.kc, kd, x);
-    load8<SRC>(p.value, vs, x);
-    store8<DST>(p.vc, vd, x);
+    if (p.unit_scale) {
+      // Same 16-bit type: copy the bits (NaN payloads included).
+      *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(p.kc) + kd) =
+          *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p.key) + ks);
+      *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(p.vc) + vd) =
+          *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p.value) + vs);
+      return;
+    }
   }
+  float x[8];
+  load8<SRC>(p.key, ks, x);
+  if (!p.unit_scale) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = div_rn(x[e], p.k_scale, p.k_rcp);
+  }
+  store8<DST>(p.kc, kd, x);
+  load8<SRC>(p.value, vs, x);
+  if (!p.unit_scale) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = div_rn(x[e], p.v_scale, p.v_rcp);
+  }
+  store8<DST>(p.vc, vd, x);
 }
 
 template <int SRC, int DST>
@@ -120,6 +186,7 @@ static hipError_t launch_w_src(const WriteParams& p, hipStream_t stream) {
     case kF16: return launch_w<SRC, kF16>(p, stream);
     case kBF16: return launch_w<SRC, kBF16>(p, stream);
     case kF32: return launch_w<SRC, kF32>(p, stream);
+    case kFP8: return launch_w<SRC, kFP8>(p, stream);
     default: return hipErrorInvalidValue;
   }
 }

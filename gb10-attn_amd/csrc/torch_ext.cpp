@@ -11,7 +11,8 @@
 //   paged_attention_prefill       kernels/paged_attn_prefill.h:13-15
 //   paged_attention_prefill_wmma  kernels/paged_attn_wmma.h:13-15
 // plus paged_attention_prefill_varlen (mixed decode + prefill batches) and
-// write_kv (the engine's KV-cache write, pa_write_kv).  As in the
+// write_kv / write_kv_scaled (the engine's KV-cache write, pa_write_kv and
+// pa_write_kv_scaled).  As in the
 // reference, inputs are made contiguous (K/V only when the kernels cannot
 // address the given strides), block tables and context lengths are cast to
 // int32, and the v3 scratch comes from the caching allocator per call.  Work
@@ -176,8 +177,8 @@ int64_t op_choose_num_splits(int64_t num_seqs, int64_t num_heads, int64_t max_co
   return s;
 }
 
-void op_write_kv(at::Tensor& k_cache, at::Tensor& v_cache, const at::Tensor& key, const at::Tensor& value,
-                 const at::Tensor& slot_mapping) {
+void op_write_kv_scaled(at::Tensor& k_cache, at::Tensor& v_cache, const at::Tensor& key, const at::Tensor& value,
+                        const at::Tensor& slot_mapping, double k_scale, double v_scale) {
   TORCH_CHECK(k_cache.is_cuda() && v_cache.is_cuda() && key.is_cuda() && value.is_cuda(),
               "k_cache, v_cache, key and value must be on CUDA");
   TORCH_CHECK(kv_addressable(k_cache) && kv_addressable(v_cache),
@@ -188,7 +189,12 @@ void op_write_kv(at::Tensor& k_cache, at::Tensor& v_cache, const at::Tensor& key
   if (sm.scalar_type() != at::kInt && sm.scalar_type() != at::kLong) sm = sm.to(at::kLong);
   c10::DeviceGuard guard(key.device());
   pa_tensor_t kc = view(k_cache), vc = view(v_cache), ks = view(kk), vs = view(vv), ss = view(sm);
-  check(pa_write_kv(&kc, &vc, &ks, &vs, &ss, stream_of(kk)));
+  check(pa_write_kv_scaled(&kc, &vc, &ks, &vs, &ss, k_scale, v_scale, stream_of(kk)));
+}
+
+void op_write_kv(at::Tensor& k_cache, at::Tensor& v_cache, const at::Tensor& key, const at::Tensor& value,
+                 const at::Tensor& slot_mapping) {
+  op_write_kv_scaled(k_cache, v_cache, key, value, slot_mapping, 1.0, 1.0);
 }
 
 }  // namespace
@@ -213,4 +219,7 @@ TORCH_LIBRARY(gb10_attn, m) {
         &op_paged_attention_prefill_varlen);
   m.def("write_kv(Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor key, Tensor value, Tensor slot_mapping) -> ()",
         &op_write_kv);
+  m.def("write_kv_scaled(Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor key, Tensor value, Tensor slot_mapping, "
+        "float k_scale, float v_scale) -> ()",
+        &op_write_kv_scaled);
 }

@@ -195,11 +195,13 @@ def plan_partitions(num_seqs, num_heads, num_kv_heads, head_dim, max_context, nu
     return int(a.value), int(b.value)
 
 
-def write_kv(k_cache, v_cache, key, value, slot_mapping):
+def write_kv(k_cache, v_cache, key, value, slot_mapping, k_scale=1.0, v_scale=1.0):
     """KV-cache write: key/value [T, HKV, D] (fp32/fp16/bf16, any token/head
     strides) into k_cache/v_cache [NB, BS, HKV, D] at slot_mapping[t]
     (block slot // BS, row slot % BS; negative slots skipped), converted to the
-    cache dtype with round-to-nearest-even.  In place; returns nothing."""
+    cache dtype with round-to-nearest-even.  With scales the cache receives
+    key / k_scale and value / v_scale (pa_write_kv_scaled); an FP8 E4M3 cache
+    saturates at +-448.  In place; returns nothing."""
     for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache"), (key, "key"), (value, "value")):
         if not t.is_cuda:
             raise RuntimeError(f"{n} must be on CUDA")
@@ -215,16 +217,17 @@ def write_kv(k_cache, v_cache, key, value, slot_mapping):
         slot_mapping = slot_mapping.to(torch.int64)
     slot_mapping = slot_mapping.to(key.device).contiguous()
     with torch.cuda.device(key.device):
-        check(lib().pa_write_kv(C.byref(view(k_cache)), C.byref(view(v_cache)), C.byref(view(key)),
-                                C.byref(view(value)), C.byref(view(slot_mapping)), _stream(key.device)))
+        check(lib().pa_write_kv_scaled(C.byref(view(k_cache)), C.byref(view(v_cache)), C.byref(view(key)),
+                                       C.byref(view(value)), C.byref(view(slot_mapping)), float(k_scale),
+                                       float(v_scale), _stream(key.device)))
 
 
-def write_kv_blocks(kv_pool, block_ids, start, k, v):
+def write_kv_blocks(kv_pool, block_ids, start, k, v, k_scale=1.0, v_scale=1.0):
     """The serving engine's write_kv(block_ids, start, k, v): one sequence's
     K/V for all layers, k/v [n_layer, n_head, ctx, head_dim] (host numpy or
     torch), into kv_pool [n_layer, 2, NB, BS, HKV, D] at token positions
     start .. start + ctx - 1 of the sequence whose pages are block_ids.  Each
-    layer is one pa_write_kv call on the [ctx, HKV, D] view of k[layer]."""
+    layer is one pa_write_kv_scaled call on the [ctx, HKV, D] view of k[layer]."""
     L, _, NB, BS, HKV, D = kv_pool.shape
     k = torch.as_tensor(k).to(kv_pool.device)
     v = torch.as_tensor(v).to(kv_pool.device)
@@ -235,7 +238,8 @@ def write_kv_blocks(kv_pool, block_ids, start, k, v):
         raise RuntimeError("block_ids do not cover the written positions")
     slots = blocks[pos // BS] * BS + pos % BS
     for layer in range(L):
-        write_kv(kv_pool[layer, 0], kv_pool[layer, 1], k[layer].permute(1, 0, 2), v[layer].permute(1, 0, 2), slots)
+        write_kv(kv_pool[layer, 0], kv_pool[layer, 1], k[layer].permute(1, 0, 2), v[layer].permute(1, 0, 2), slots,
+                 k_scale, v_scale)
 
 
 def torch_ops():

@@ -238,7 +238,8 @@ int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const
  * k_cache / v_cache ([NB, BS, HKV, D] views, as the attention entry points
  * take them), converted to the cache's type with round-to-nearest-even.
  * A negative slot (padding) or one >= NB * BS is skipped.  slot_mapping is
- * int32 or int64; key/value and the caches are float32, float16 or bfloat16.
+ * int32 or int64; key/value are float32, float16 or bfloat16, the caches
+ * float32, float16, bfloat16 or float8_e4m3fn (see pa_write_kv_scaled).
  * Replaces the reference engine's TorchBlockAllocator.write_kv (external to
  * the reference; its call sites are harness/repro_crash.py:52-58 and
  * results/c001-20260901-223111/bench_b64_c2048.txt:16-22): one sequence's
@@ -246,6 +247,18 @@ int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const
  * slot_mapping[t] = block_ids[t / BS] * BS + t % BS. */
 int pa_write_kv(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tensor_t* key,
                 const pa_tensor_t* value, const pa_tensor_t* slot_mapping, void* stream);
+
+/* pa_write_kv into a scaled cache: the cache receives key / k_scale and
+ * value / v_scale (fp32 division, correctly rounded, then the cache type's
+ * rounding), the quantised form paged_attention_v3_scaled reads back.  With
+ * an FP8 E4M3 cache (also accepted by pa_write_kv, scale 1) each value is
+ * rounded to nearest even and saturated at +-448 (infinities too), NaN is
+ * stored as 0x7f.  Scales must be finite and nonzero.  The reference has no
+ * FP8 path (docs/REPORT.md:270); the engine's write it extends is the one
+ * pa_write_kv replaces (harness/repro_crash.py:52-58). */
+int pa_write_kv_scaled(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tensor_t* key,
+                       const pa_tensor_t* value, const pa_tensor_t* slot_mapping, double k_scale,
+                       double v_scale, void* stream);
 
 #ifdef __cplusplus
 }

@@ -305,24 +305,31 @@ def prefill(q, k, v, bt, ctx, scale, kv_dtype="f32") -> np.ndarray:
     return out
 
 
-def write_kv(k_cache, v_cache, key, value, slots, cache_dtype, src_dtype):
+def write_kv(k_cache, v_cache, key, value, slots, cache_dtype, src_dtype, k_scale=1.0, v_scale=1.0):
     """KV-cache write, in place on host caches [NB, BS, HKV, D] (storage per NP_OF):
     token t's rows key[t], value[t] ([T, HKV, D], stored as src_dtype) go to
     block slots[t] // BS, row slots[t] % BS, rounded to the cache type (round
-    to nearest even; the same 16-bit type is copied bit for bit).  A negative
+    to nearest even; FP8 E4M3 saturating at +-448 as fp8_encode; the same
+    16-bit type at scale 1 is copied bit for bit).  With scales the cache
+    receives key / k_scale and value / v_scale, divided in float32.  A negative
     slot or one >= NB * BS is skipped.  This restates the serving engine's
     write_kv layout (token j of a sequence -> block_ids[j // BS], row j % BS;
     external to the reference, called at harness/repro_crash.py:52-58)."""
     NB, BS = k_cache.shape[:2]
+    unit = np.float32(k_scale) == 1 and np.float32(v_scale) == 1
     for t, s in enumerate(np.asarray(slots).tolist()):
         if s < 0 or s >= NB * BS:
             continue
         b, o = divmod(int(s), BS)
-        for cache, src in ((k_cache, key), (v_cache, value)):
-            if src_dtype == cache_dtype:
+        for cache, src, sc in ((k_cache, key, k_scale), (v_cache, value, v_scale)):
+            if src_dtype == cache_dtype and unit:
                 cache[b, o] = src[t]
             else:
-                cache[b, o] = quantize(to_float(src[t], src_dtype), cache_dtype)
+                x = to_float(src[t], src_dtype)
+                with np.errstate(invalid="ignore", over="ignore"):
+                    if not unit:
+                        x = (x / np.float32(sc)).astype(np.float32)
+                    cache[b, o] = quantize(x, cache_dtype)
 
 
 def gather(k, v, bt_row, n, kvh, kv_dtype="f32"):

@@ -235,7 +235,7 @@ def write_call(pa, a):
 
 
 @pytest.mark.parametrize("case,code,msg", [
-    (dict(cdt=F64), 1, "k_cache must be float16, bfloat16 or float32"),
+    (dict(cdt=F64), 1, "k_cache must be float16, bfloat16, float32 or float8_e4m3fn"),
     (dict(sdt=I32), 1, "key must be float16, bfloat16 or float32"),
     (dict(slot=F32), 1, "slot_mapping must be int32 or int64"),
     (dict(D=60), 2, "head_dim must be a positive multiple of 8"),
@@ -269,6 +269,17 @@ def test_write_kv_shape_rejections(pa):
     a["key"].dtype = F16
     rc, err = write_call(pa, write_args(pa, sdt=F16) | {"key": a["key"]})
     assert rc == 2 and "multiples of 16 bytes" in err
+
+
+@pytest.mark.parametrize("ks,vs", [(0.0, 1.0), (1.0, float("inf")), (float("nan"), 1.0), (1e-50, 1.0)])
+def test_write_kv_scaled_rejects_bad_scales(pa, ks, vs):
+    """Scales must be finite and nonzero (as float32: 1e-50 rounds to 0); refused before any HIP call."""
+    a = write_args(pa, cdt=6)
+    L = pa.lib()
+    rc = L.pa_write_kv_scaled(C.byref(a["kc"]), C.byref(a["vc"]), C.byref(a["key"]), C.byref(a["val"]),
+                              C.byref(a["slots"]), ks, vs, None)
+    err = L.pa_last_error().decode()
+    assert rc == 1 and "k_scale and v_scale must be finite and nonzero" in err, (rc, err)
 
 
 def test_write_kv_zero_tokens_is_a_no_op(pa):

@@ -66,6 +66,23 @@ def test_write_kv_op(pa, dev):
     assert np.array_equal(kc.cpu().numpy(), wk) and np.array_equal(vc.cpu().numpy(), wv)
 
 
+def test_write_kv_scaled_op(pa, dev):
+    """torch.ops.gb10_attn.write_kv_scaled into an FP8 cache equals the oracle's scaled write."""
+    ops = pa.torch_ops()
+    g = torch.Generator().manual_seed(37)
+    key = torch.randn(40, 2, 64, generator=g) * 5
+    val = torch.randn(40, 2, 64, generator=g) * 5
+    slots = torch.randperm(6 * 16, generator=g)[:40]
+    kc = torch.zeros(6, 16, 2, 64, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    vc = torch.zeros_like(kc)
+    ops.write_kv_scaled(kc, vc, key.to(dev), val.to(dev), slots.to(dev), 0.25, 0.02)
+    wk = np.zeros((6, 16, 2, 64), np.uint8)
+    wv = np.zeros_like(wk)
+    oracle.write_kv(wk, wv, key.numpy(), val.numpy(), slots.numpy(), "fp8", "f32", k_scale=0.25, v_scale=0.02)
+    assert np.array_equal(kc.view(torch.uint8).cpu().numpy(), wk)
+    assert np.array_equal(vc.view(torch.uint8).cpu().numpy(), wv)
+
+
 def test_reference_error_messages(pa, dev):
     ops = pa.torch_ops()
     inp = decode_case(1, 8, 4, 64, 16, [20], seed=36)

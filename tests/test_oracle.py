@@ -464,3 +464,26 @@ def test_fp8_codec_matches_torch():
     want = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
     assert np.array_equal(oracle.fp8_encode(x), want)
     assert list(oracle.fp8_encode(np.float32([470, 1e6, -500, np.nan]))) == [0x7E, 0x7E, 0xFE, 0x7F]
+    specials = np.float32([-0.0, 0.0, -np.inf, np.inf, 448, 464, 1e-30, -1e-30, 2.0 ** -10, 3 * 2.0 ** -10])
+    assert list(oracle.fp8_encode(specials)) == [0x80, 0x00, 0xFE, 0x7E, 0x7E, 0x7E, 0x00, 0x80, 0x00, 0x02]
+
+
+@pytest.mark.parametrize("cache", ["fp8", "f16", "bf16"])
+def test_write_kv_scaled_matches_torch(cache):
+    """oracle.write_kv with per-tensor scales stores (x / scale) rounded to the
+    cache type, as torch computes it independently (float32 division, then the
+    cast), for values inside the FP8 range."""
+    rng = np.random.default_rng(4)
+    NB, BS, HKV, D, T = 6, 4, 2, 8, 20
+    key = (rng.standard_normal((T, HKV, D)) * 3).astype(np.float32)
+    val = (rng.standard_normal((T, HKV, D)) * 3).astype(np.float32)
+    slots = rng.permutation(NB * BS)[:T]
+    kc = np.zeros((NB, BS, HKV, D), oracle.NP_OF[cache])
+    vc = np.zeros_like(kc)
+    oracle.write_kv(kc, vc, key, val, slots, cache, "f32", k_scale=0.05, v_scale=3.7)
+    tdt = {"fp8": torch.float8_e4m3fn, "f16": torch.float16, "bf16": torch.bfloat16}[cache]
+    for c, x, sc in ((kc, key, 0.05), (vc, val, 3.7)):
+        want = (torch.from_numpy(x) / torch.tensor(sc, dtype=torch.float32)).to(tdt)
+        got = torch.from_numpy(c.reshape(NB * BS, HKV, D)[slots]).view(tdt) if cache != "f16" else \
+            torch.from_numpy(c.reshape(NB * BS, HKV, D)[slots])
+        assert torch.equal(got.view(torch.uint8) if cache == "fp8" else got, want.view(torch.uint8) if cache == "fp8" else want)
