@@ -177,8 +177,9 @@ class PrefillWorkload:
     pool, then the last S positions attended (ctx = S: a whole prompt; ctx > S:
     a trailing chunk, kernels/paged_attn_prefill.cu:62-64)."""
 
-    def __init__(self, pa, *, B, S, H, HKV, D, BS, dtype, seed, name, ctx=None):
+    def __init__(self, pa, *, B, S, H, HKV, D, BS, dtype, seed, name, ctx=None, cache_dtype=None, kv_scale=None):
         self.pa, self.name = pa, name
+        self.kv_scale = kv_scale  # scaled (FP8) pool: it holds K / kv_scale and V / kv_scale
         ctx = ctx or S
         dev = torch.device("cuda:0")
         g = torch.Generator(device=dev)
@@ -191,12 +192,17 @@ class PrefillWorkload:
         k_new = torch.randn((B, ctx, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
         v_new = torch.randn((B, ctx, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
         # Write the prompt's K/V into the paged pool with pa_write_kv (untimed setup).
-        self.k = torch.zeros((nb, BS, HKV, D), device=dev, dtype=dtype)
+        if cache_dtype == torch.float8_e4m3fn:
+            self.k = torch.zeros((nb, BS, HKV, D), device=dev, dtype=torch.uint8).view(cache_dtype)
+        else:
+            self.k = torch.zeros((nb, BS, HKV, D), device=dev, dtype=dtype)
         self.v = torch.zeros_like(self.k)
         tok = torch.arange(ctx, device=dev)
         bt = torch.from_numpy(perm).to(dev)
         slots = (bt[:, tok // BS].long() * BS + tok % BS).reshape(-1)
-        pa.write_kv(self.k, self.v, k_new.reshape(B * ctx, HKV, D), v_new.reshape(B * ctx, HKV, D), slots)
+        ks = kv_scale or 1.0
+        pa.write_kv(self.k, self.v, k_new.reshape(B * ctx, HKV, D), v_new.reshape(B * ctx, HKV, D), slots,
+                    k_scale=ks, v_scale=ks)
         self.bt = bt
         self.ctx = torch.full((B,), ctx, dtype=torch.int32, device=dev)
         self.out = torch.empty((B, S, H, D), device=dev, dtype=dtype)
@@ -210,7 +216,11 @@ class PrefillWorkload:
         self.L = pa.lib()
 
     def launch(self, i, stream, ev_mid=None):
-        rc = self.L.paged_attention_prefill_wmma(*self.args, self.scale, stream)
+        if self.kv_scale:
+            rc = self.L.paged_attention_prefill_wmma_scaled(*self.args, self.scale, self.kv_scale, self.kv_scale,
+                                                             stream)
+        else:
+            rc = self.L.paged_attention_prefill_wmma(*self.args, self.scale, stream)
         if rc != 0:
             raise RuntimeError(self.pa.last_error())
 
@@ -283,7 +293,7 @@ def check_prefill(work, rows=(0, 1, 63, 64, 127, 128, 129, 511, -2, -1)):
     bs = [b for b in (0, B - 1) for _ in rs]
     rr = [r for _ in (0, B - 1) for r in rs]
     pos = np.asarray([int(ctx[b]) - S + r for b, r in zip(bs, rr)], np.int32)
-    k, v, bts = _gather_pages(work.k, work.v, bt[bs], pos + 1, work.k.shape[1])
+    k, v, bts = _gather_pages(work.k, work.v, bt[bs], pos + 1, work.k.shape[1], work.kv_scale)
     want = oracle.decode(work.q.float().cpu().numpy()[bs, rr], k, v, bts, pos + 1, work.scale, "f32")
     got = work.out.float().cpu().numpy()[bs, rr]
     return _compare(got, want, f"{len(rr)} query rows of sequences 0 and {B - 1} vs oracle.decode of their prefix"), kernels
@@ -397,6 +407,9 @@ PREFILL_CFG = {
     "prefill_c4a": dict(B=8, S=1024, H=12, HKV=12, D=64, dtype=torch.float16, seed=4),
     "prefill_c4b": dict(B=2, S=4096, H=32, HKV=32, D=128, dtype=torch.bfloat16, seed=6),
     "prefill_ref_chunk": dict(B=4, S=512, ctx=2048, H=12, HKV=12, D=64, dtype=torch.float16, seed=7),
+    # Config 4b's geometry over an FP8 E4M3 pool (per-tensor scale 1/16, bf16 q): tiles converted to fp16.
+    "prefill_c4b_fp8": dict(B=2, S=4096, H=32, HKV=32, D=128, dtype=torch.bfloat16, seed=6,
+                            cache_dtype=torch.float8_e4m3fn, kv_scale=1.0 / 16),
 }
 
 # The prompt K/V of configs 4a and 4b written into their paged pools.
@@ -993,7 +1006,8 @@ def prefill_record(work, steps, warmup):
         "ms_per_step": round(ms, 5),
         "kernel_ms": round(kms, 5), "flops_per_step": work.flops,
         "prompt_tokens_per_s": round(work.q.shape[0] * work.q.shape[1] / (ms * 1e-3), 1),
-        "dtype": str(work.dtype).replace("torch.", ""), "kernels": kernels, "check": chk,
+        "dtype": str(work.dtype).replace("torch.", ""),
+        "kv_dtype": str(work.k.dtype).replace("torch.", ""), "kernels": kernels, "check": chk,
     }
 
 
@@ -1005,7 +1019,7 @@ def main():
     ap.add_argument("--pools", type=int, default=6, help="rotated KV pools (config 2)")
     ap.add_argument("--workload", default="decode_c2",
                     choices=["decode_c2", "decode_c2_fp32io", "decode_c3", "decode_c5", "decode_c2_fp8", "decode_c3_fp8", "decode_gqa8",
-                             "decode_c2_split", "sweep", "prefill_c4a", "prefill_c4b", "prefill_ref_chunk",
+                             "decode_c2_split", "sweep", "prefill_c4a", "prefill_c4b", "prefill_ref_chunk", "prefill_c4b_fp8",
                              "write_kv_c4a", "write_kv_c4b", "write_kv_c4b_fp8", "call_overhead", "mixed_c2", "copy_calib"],
                     help="with --only: run just this workload's kernel loop (for profiling)")
     ap.add_argument("--only", action="store_true", help="time only --workload, print its record")

@@ -26,7 +26,8 @@ EXPORTS = (
     "paged_attention_v3_noalloc",
     "pa_v3_partition", "pa_v3_reduce",
     "choose_num_splits", "choose_num_splits_for", "pa_plan_partitions",
-    "paged_attention_prefill", "paged_attention_prefill_wmma", "paged_attention_prefill_varlen",
+    "paged_attention_prefill", "paged_attention_prefill_wmma", "paged_attention_prefill_wmma_scaled",
+    "paged_attention_prefill_varlen",
     "pa_write_kv", "pa_write_kv_scaled",
 )
 
@@ -97,6 +98,8 @@ def lib() -> C.CDLL:
     L.choose_num_splits_for.argtypes = [i64, i64, i64, i64]
     L.pa_plan_partitions.restype = C.c_int
     L.pa_plan_partitions.argtypes = [i64, i64, i64, i64, i64, i64, C.POINTER(i64), C.POINTER(i64)]
+    L.paged_attention_prefill_wmma_scaled.restype = C.c_int
+    L.paged_attention_prefill_wmma_scaled.argtypes = six + [C.c_double, C.c_double, C.c_double, P]
     L.paged_attention_prefill_varlen.restype = C.c_int
     L.paged_attention_prefill_varlen.argtypes = six + [T, i64, C.c_double, P]
     L.pa_write_kv.restype = C.c_int

@@ -492,11 +492,12 @@ int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const p
 // MFMA prefill launch for checked arguments; cu != null selects the
 // variable-length layout (rows cu[b] .. cu[b+1] of a packed [T, H, D] q/out).
 int run_prefill_mfma(DecodeArgs& a, const pa_tensor_t* q, const int32_t* cu, int64_t T, double scale,
-                     void* stream, bool route_single = false) {
+                     void* stream, bool route_single = false, double v_scale = 1.0) {
   if (!route_single) g_launches.clear();
-  // kernels/paged_attn_wmma.cu:220-223 requires fp16; bf16 is served as well.
-  if (a.kv_dtype != kF16 && a.kv_dtype != kBF16)
-    return fail(PA_ERR_INVALID_ARGUMENT, "the MFMA path needs an fp16 or bf16 KV cache");
+  // kernels/paged_attn_wmma.cu:220-223 requires fp16; bf16 and FP8 (E4M3, read
+  // as fp16) are served as well.
+  if (a.kv_dtype != kF16 && a.kv_dtype != kBF16 && a.kv_dtype != kFP8)
+    return fail(PA_ERR_INVALID_ARGUMENT, "the MFMA path needs an fp16, bf16 or float8_e4m3fn KV cache");
   if (a.p.D > 256) return fail(PA_ERR_UNSUPPORTED, "unsupported head_dim for the MFMA path: %d", a.p.D);
   if ((int64_t)a.p.B * a.p.Sq * a.p.H == 0) return PA_OK;
   if ((reinterpret_cast<uintptr_t>(q->data) & 15) != 0)
@@ -511,11 +512,13 @@ int run_prefill_mfma(DecodeArgs& a, const pa_tensor_t* q, const int32_t* cu, int
   pp.bt_stride = p.bt_stride; pp.num_blocks = p.num_blocks;
   pp.B = p.B; pp.S = p.Sq; pp.H = p.H; pp.HKV = p.HKV; pp.G = p.G; pp.D = p.D; pp.BS = p.BS; pp.MB = p.MB;
   pp.q_dtype = p.q_dtype; pp.out_dtype = p.out_dtype;
-  pp.q_split = p.q_dtype != a.kv_dtype;
+  // FP8 K tiles take q's type when q is fp16 or bf16 (the codes convert exactly to both).
+  pp.q_split = a.kv_dtype == kFP8 ? p.q_dtype == kF32 : p.q_dtype != a.kv_dtype;
   pp.bs_div = p.bs_div;
   pp.cu_q = cu;
   pp.q_total = T;
   pp.skip_single = route_single ? 1 : 0;
+  pp.vscale = (float)v_scale;
   // The kernel applies the sign of the scale to q (exactly) and keeps the
   // softmax scale positive, so the running max of raw scores orders as the scaled ones.
   const double log2e = 1.4426950408889634;
@@ -687,6 +690,20 @@ int paged_attention_prefill_wmma(pa_tensor_t* out, const pa_tensor_t* q,
   return run_prefill_mfma(a, q, nullptr, 0, scale, stream);
 }
 
+int paged_attention_prefill_wmma_scaled(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                                        const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                                        const pa_tensor_t* context_lens, double scale, double k_scale,
+                                        double v_scale, void* stream) {
+  if (!std::isfinite(k_scale) || !std::isfinite(v_scale))
+    return fail(PA_ERR_INVALID_ARGUMENT, "k_scale and v_scale must be finite");
+  // k_scale joins the softmax scale (q . (k_scale k) = (scale k_scale) q . k),
+  // v_scale multiplies the output rows.
+  DecodeArgs a;
+  int rc = check_args(out, q, k_cache, v_cache, block_tables, context_lens, scale * k_scale, true, &a);
+  if (rc) return rc;
+  return run_prefill_mfma(a, q, nullptr, 0, scale * k_scale, stream, false, v_scale);
+}
+
 int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
                                    const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
                                    const pa_tensor_t* context_lens, const pa_tensor_t* cu_seqlens_q,
@@ -724,7 +741,7 @@ int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const
   // decode kernel, one launch over every sequence in which the others' work-
   // groups exit at once; the prefill kernel then skips them.  The rows are
   // told apart on the device (cu_seqlens_q is device memory: no host sync).
-  const bool prefill_ok = (a.kv_dtype == kF16 || a.kv_dtype == kBF16) && a.p.D <= 256 &&
+  const bool prefill_ok = (a.kv_dtype == kF16 || a.kv_dtype == kBF16 || a.kv_dtype == kFP8) && a.p.D <= 256 &&
                           (reinterpret_cast<uintptr_t>(q->data) & 15) == 0 && (int64_t)a.p.B * a.p.H > 0;
   if (prefill_ok) {  // (otherwise the prefill call below reports why, before any launch)
     DecodeArgs d = a;

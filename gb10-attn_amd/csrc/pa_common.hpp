@@ -104,6 +104,7 @@ struct PrefillParams {
   FastDiv bs_div;
   float qscale;      // |scale| * log2(e), or 1 when scale == 0 (always positive)
   float q_sign;      // sign of scale applied to q (+1, -1, or 0 when scale == 0)
+  float vscale;      // v_scale of a scaled (FP8) cache: multiplies the output rows
   uint32_t q_and;    // the same on packed 16-bit q: bits & q_and ^ q_xor
   uint32_t q_xor;
 };

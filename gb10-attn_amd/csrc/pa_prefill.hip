@@ -131,10 +131,26 @@ enum PvMode : int {
   kPvDirect = 0,   // V tile loaded straight into LDS; P and V in fp16
   kPvConvert = 1,  // bf16 V converted to fp16 while staged; P and V in fp16
   kPvSplit = 2,    // bf16 V in LDS; P as bf16 hi + lo, two products
+  kPvF8 = 3,       // FP8 K and V codes staged in registers, written to LDS as fp16 (exact)
 };
 template <int M>
 struct PvTag {
   static constexpr int value = M;
+};
+
+// FP8 (E4M3) caches: the codes convert exactly to fp16 and to bf16, so K tiles
+// take q's 16-bit type (no hi + lo split of a bf16 q) and V tiles fp16 (P
+// stays fp16).  KvFP8 serves fp16 and fp32 q, KvFP8QkBf16 bf16 q.
+struct KvFP8QkBf16 : KvFP8 {
+  static constexpr const char* kName = "pa::KvFP8QkBf16";
+};
+template <typename KV>
+struct QkBf16 {  // Q.K^T on bf16 MFMA
+  static constexpr bool value = KV::kCode == kBF16;
+};
+template <>
+struct QkBf16<KvFP8QkBf16> {
+  static constexpr bool value = true;
 };
 
 template <int D>
@@ -197,7 +213,9 @@ void prefill_mfma_kernel(const PrefillParams p) {
   constexpr int MTW = kSplit ? 1 : MT;           // 32-key m-tiles of each tile this wave computes
   constexpr int QB = kSplit ? 2 * QW : Sh::QB;   // query rows per work-group
   constexpr int NCH = Sh::NCH, CPT = Sh::CPT;
-  constexpr bool kBf16 = KV::kCode == kBF16;
+  constexpr bool kBf16 = QkBf16<KV>::value;  // Q.K^T operand type (and the type of a split q)
+  constexpr bool kF8 = KV::kCode == kFP8;    // tiles converted from FP8 codes; P.V in fp16
+  constexpr int EB = KV::kBytes;
 
   __shared__ __attribute__((aligned(16))) uint16_t sK0[KB * D];
   __shared__ __attribute__((aligned(16))) uint16_t sK1[KB * D];
@@ -342,10 +360,10 @@ void prefill_mfma_kernel(const PrefillParams p) {
     }
   };
 
-  const char* kbase = static_cast<const char*>(p.k) + (int64_t)kvh * p.k_sh * 2;
-  const char* vbase = static_cast<const char*>(p.v) + (int64_t)kvh * p.v_sh * 2;
-  const uint32_t k_sbb = (uint32_t)(p.k_sb * 2), k_stb = (uint32_t)(p.k_st * 2);
-  const uint32_t v_sbb = (uint32_t)(p.v_sb * 2), v_stb = (uint32_t)(p.v_st * 2);
+  const char* kbase = static_cast<const char*>(p.k) + (int64_t)kvh * p.k_sh * EB;
+  const char* vbase = static_cast<const char*>(p.v) + (int64_t)kvh * p.v_sh * EB;
+  const uint32_t k_sbb = (uint32_t)(p.k_sb * EB), k_stb = (uint32_t)(p.k_st * EB);
+  const uint32_t v_sbb = (uint32_t)(p.v_sb * EB), v_stb = (uint32_t)(p.v_st * EB);
   const uint64_t nb = (uint64_t)p.num_blocks;
 
   // This thread's chunks of a tile: chunk c fills LDS chunk position
@@ -357,8 +375,8 @@ void prefill_mfma_kernel(const PrefillParams p) {
   for (int c = 0; c < CPT; ++c) {
     const int pos = (c * 4 + wave) * 64 + lane;
     prow[c] = pos / NCH;
-    ksrc[c] = kpos<D>(prow[c], pos % NCH) * 16;
-    vsrc[c] = vpos<D>(prow[c], pos % NCH) * 16;
+    ksrc[c] = kpos<D>(prow[c], pos % NCH) * 8 * EB;  // byte offset of the 8-element source chunk
+    vsrc[c] = vpos<D>(prow[c], pos % NCH) * 8 * EB;
   }
   int badkey = 0x7fffffff;
 
@@ -394,7 +412,7 @@ void prefill_mfma_kernel(const PrefillParams p) {
   // cannot hold, or non-finite data): the caller reruns in kPvSplit.
   auto run = [&](auto mode_tag) -> bool {
     constexpr int kMode = decltype(mode_tag)::value;
-    constexpr bool kDirectV = kMode != kPvConvert;
+    constexpr bool kDirectV = kMode != kPvConvert && kMode != kPvF8;
     constexpr bool kPvBf16 = kMode == kPvSplit;
 
 #pragma unroll
@@ -405,7 +423,8 @@ void prefill_mfma_kernel(const PrefillParams p) {
     m = -__builtin_inff();
     l = 0.0f;
 
-    u32x4_t vreg[kDirectV ? 1 : CPT];
+    u32x4_t vreg[kDirectV || kMode == kPvF8 ? 1 : CPT];
+    u32x2_t kreg8[kMode == kPvF8 ? CPT : 1], vreg8[kMode == kPvF8 ? CPT : 1];  // FP8 codes of this thread's chunks
     uint32_t umask = 0;
 
     // Loads of a tile into (dK, dV) from its offset table: entries() reads
@@ -420,8 +439,13 @@ void prefill_mfma_kernel(const PrefillParams p) {
     auto chunk = [&](int c, uint16_t* dK, uint16_t* dV) {
       const uint32_t use = (uint32_t)ent[c][1] & 1u;
       umask |= use << c;
-      lds_dma16(kbase + ent[c][0] + ksrc[c], (lds_void_t*)(dK + (c * 4 + wave) * 512));
       const char* va = vbase + (ent[c][1] - use) + vsrc[c];
+      if constexpr (kMode == kPvF8) {
+        kreg8[c] = *reinterpret_cast<const u32x2_t*>(kbase + ent[c][0] + ksrc[c]);
+        vreg8[c] = *reinterpret_cast<const u32x2_t*>(va);
+        return;
+      }
+      lds_dma16(kbase + ent[c][0] + ksrc[c], (lds_void_t*)(dK + (c * 4 + wave) * 512));
       if constexpr (kDirectV) {
         lds_dma16(va, (lds_void_t*)(dV + (c * 4 + wave) * 512));
       } else {
@@ -438,8 +462,35 @@ void prefill_mfma_kernel(const PrefillParams p) {
     // (their probabilities are 0, but substituted data may not be finite),
     // or convert the register-staged bf16 V to fp16 (exact for
     // 2^-17 <= |v| < 65504; smaller values round to fp16 subnormals).
-    auto finish = [&](uint16_t* dV) {
-      if constexpr (kDirectV) {
+    auto finish = [&](uint16_t* dK, uint16_t* dV) {
+      if constexpr (kMode == kPvF8) {
+        // Codes -> 16-bit pairs (v_cvt_scalef32_pk_{f16,bf16}_fp8 at scale 1:
+        // exact for every code), K in the Q.K^T type, V in fp16; V rows that were
+        // substituted are zeroed (their codes may be NaN), K rows need not be
+        // (their scores are masked).
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+          uint32_t wk[4], wv[4];
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            if constexpr (kBf16) {
+              wk[2 * j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kreg8[c][j], 1.0f, false));
+              wk[2 * j + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kreg8[c][j], 1.0f, true));
+            } else {
+              wk[2 * j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(kreg8[c][j], 1.0f, false));
+              wk[2 * j + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(kreg8[c][j], 1.0f, true));
+            }
+            wv[2 * j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(vreg8[c][j], 1.0f, false));
+            wv[2 * j + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(vreg8[c][j], 1.0f, true));
+          }
+          const bool used = (umask >> c) & 1u;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) wv[j] = used ? wv[j] : 0u;
+          const int at = ((c * 4 + wave) * 64 + lane) * 8;
+          *reinterpret_cast<u32x4_t*>(dK + at) = u32x4_t{wk[0], wk[1], wk[2], wk[3]};
+          *reinterpret_cast<u32x4_t*>(dV + at) = u32x4_t{wv[0], wv[1], wv[2], wv[3]};
+        }
+      } else if constexpr (kDirectV) {
         if (umask != (1u << CPT) - 1u) {
 #pragma unroll
           for (int c = 0; c < CPT; ++c) {
@@ -592,7 +643,7 @@ void prefill_mfma_kernel(const PrefillParams p) {
     if (ntiles > 0) {
       issue(s_off0, sK0, sV0);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's loads are in LDS
-      finish(sV0);
+      finish(sK0, sV0);
     }
     __syncthreads();
     for (int t = 0; t < ntiles; t += 2) {
@@ -603,7 +654,7 @@ void prefill_mfma_kernel(const PrefillParams p) {
       if (t * KB + par * 32 < wave_kend) compute(t, sK0, sV0);
       if (more1) {
         __builtin_amdgcn_s_waitcnt(0x0F70);
-        finish(sV1);
+        finish(sK1, sV1);
       }
       __syncthreads();
       if (!more1) break;
@@ -614,7 +665,7 @@ void prefill_mfma_kernel(const PrefillParams p) {
       if ((t + 1) * KB + par * 32 < wave_kend) compute(t + 1, sK1, sV1);
       if (t + 2 < ntiles) {
         __builtin_amdgcn_s_waitcnt(0x0F70);
-        finish(sV0);
+        finish(sK0, sV0);
       }
       __syncthreads();
     }
@@ -632,7 +683,9 @@ void prefill_mfma_kernel(const PrefillParams p) {
     return true;
   };
 
-  if constexpr (kBf16) {
+  if constexpr (kF8) {
+    run(PvTag<kPvF8>{});
+  } else if constexpr (kBf16) {
     if (!run(PvTag<kPvConvert>{})) {
       badkey = 0x7fffffff;
       run(PvTag<kPvSplit>{});
@@ -680,7 +733,7 @@ void prefill_mfma_kernel(const PrefillParams p) {
   const float lt = l + __shfl_xor(l, 32, 64);
   if (!live) return;
   const bool bad = bad_from <= qpos;
-  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  const float inv = lt > 0.0f ? p.vscale / lt : 0.0f;
   const int64_t orow = ((tok0 + qrow) * p.H + h) * D;
   // Slots 4j .. 4j+3 of m-tile dt are 4 consecutive dims: one 8-byte (16-bit
   // out) or 16-byte (fp32 out) store when the output base allows it.
@@ -796,6 +849,7 @@ static hipError_t launch_pf_kv(const PrefillParams& p, hipStream_t stream) {
 hipError_t launch_prefill_mfma(const PrefillParams& p, int kv_dtype, hipStream_t stream) {
   if (kv_dtype == kF16) return launch_pf_kv<KvF16>(p, stream);
   if (kv_dtype == kBF16) return launch_pf_kv<KvBF16>(p, stream);
+  if (kv_dtype == kFP8) return p.q_dtype == kBF16 ? launch_pf_kv<KvFP8QkBf16>(p, stream) : launch_pf_kv<KvFP8>(p, stream);
   return hipErrorInvalidValue;
 }
 

@@ -120,6 +120,18 @@ at::Tensor op_paged_attention_prefill_wmma(const at::Tensor& q, const at::Tensor
   return call_simple(&paged_attention_prefill_wmma, q, k, v, bt, ctx, scale, 4, "[B, S, H, D]");
 }
 
+at::Tensor op_paged_attention_prefill_wmma_scaled(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                                  const at::Tensor& bt, const at::Tensor& ctx, double scale,
+                                                  double k_scale, double v_scale) {
+  Args a = prep(q, k, v, bt, ctx, 4, "[B, S, H, D]");
+  c10::DeviceGuard guard(a.q.device());
+  at::Tensor out = at::empty(a.q.sizes(), a.q.options().dtype(at::kFloat));
+  pa_tensor_t o = view(out), qq = view(a.q), kk = view(a.k), vv = view(a.v), bb = view(a.bt), cc = view(a.ctx);
+  check(paged_attention_prefill_wmma_scaled(&o, &qq, &kk, &vv, &bb, &cc, scale, k_scale, v_scale,
+                                            stream_of(a.q)));
+  return out;
+}
+
 at::Tensor op_paged_attention_v3(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                                  const at::Tensor& bt, const at::Tensor& ctx, double scale, int64_t num_splits) {
   Args a = prep(q, k, v, bt, ctx, 3, "[B, H, D]");
@@ -214,6 +226,9 @@ TORCH_LIBRARY(gb10_attn, m) {
         "Tensor context_lens, float scale) -> Tensor", &op_paged_attention_prefill);
   m.def("paged_attention_prefill_wmma(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, "
         "Tensor context_lens, float scale) -> Tensor", &op_paged_attention_prefill_wmma);
+  m.def("paged_attention_prefill_wmma_scaled(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, "
+        "Tensor context_lens, float scale, float k_scale, float v_scale) -> Tensor",
+        &op_paged_attention_prefill_wmma_scaled);
   m.def("paged_attention_prefill_varlen(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, "
         "Tensor context_lens, Tensor cu_seqlens_q, int max_q_len, float scale) -> Tensor",
         &op_paged_attention_prefill_varlen);

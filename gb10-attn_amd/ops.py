@@ -113,10 +113,21 @@ def paged_attention_prefill(q, k_cache, v_cache, block_tables, context_lens, sca
 
 
 def paged_attention_prefill_wmma(q, k_cache, v_cache, block_tables, context_lens, scale, *,
-                                 out_dtype=torch.float32, out=None):
-    """kernels/paged_attn_wmma.h:13-15 -- causal chunked prefill on MFMA (fp16/bf16 KV)."""
-    return _call_simple(lib().paged_attention_prefill_wmma, q, k_cache, v_cache, block_tables,
-                        context_lens, scale, out_dtype, out, 4, "[B, S, H, D]")
+                                 out_dtype=torch.float32, out=None, k_scale=1.0, v_scale=1.0):
+    """kernels/paged_attn_wmma.h:13-15 -- causal chunked prefill on MFMA (fp16/bf16/FP8 KV).
+    k_scale / v_scale dequantise a scaled cache (paged_attention_prefill_wmma_scaled)."""
+    if k_scale == 1.0 and v_scale == 1.0:
+        return _call_simple(lib().paged_attention_prefill_wmma, q, k_cache, v_cache, block_tables,
+                            context_lens, scale, out_dtype, out, 4, "[B, S, H, D]")
+    q, k_cache, v_cache, block_tables, context_lens = _prep(
+        q, k_cache, v_cache, block_tables, context_lens, 4, "[B, S, H, D]")
+    o = _out(q, out_dtype, out)
+    with torch.cuda.device(q.device):
+        check(lib().paged_attention_prefill_wmma_scaled(
+            C.byref(view(o)), C.byref(view(q)), C.byref(view(k_cache)), C.byref(view(v_cache)),
+            C.byref(view(block_tables)), C.byref(view(context_lens)), float(scale), float(k_scale),
+            float(v_scale), _stream(q.device)))
+    return o
 
 
 def paged_attention_prefill_varlen(q, k_cache, v_cache, block_tables, context_lens, cu_seqlens_q,

@@ -176,10 +176,11 @@ int paged_attention_prefill(pa_tensor_t* out, const pa_tensor_t* q, const pa_ten
 
 /* Causal (chunked) prefill on CDNA4 matrix cores.  Replaces
  * paged_attention_prefill_wmma(), kernels/paged_attn_wmma.h:13-15
- * (kernels/paged_attn_wmma.cu:212-274).  K/V fp16 (as the reference) or
- * bf16; Q is rounded to the KV type (split hi + lo when it arrives in
- * another type), the probabilities to fp16 (bf16 hi + lo when a bf16 V value
- * does not fit fp16), accumulation is fp32.  D in {32, 64, 128, 256}. */
+ * (kernels/paged_attn_wmma.cu:212-274).  K/V fp16 (as the reference), bf16
+ * or FP8 E4M3 (read as fp16, exactly); Q is rounded to the tile type (split
+ * hi + lo when it arrives in another type), the probabilities to fp16 (bf16
+ * hi + lo when a bf16 V value does not fit fp16), accumulation is fp32.
+ * D in {32, 64, 128, 256}. */
 int paged_attention_prefill_wmma(pa_tensor_t* out, const pa_tensor_t* q,
                                  const pa_tensor_t* k_cache, const pa_tensor_t* v_cache,
                                  const pa_tensor_t* block_tables,
@@ -227,6 +228,17 @@ int paged_attention_v3_noalloc(pa_tensor_t* out, const pa_tensor_t* q, const pa_
  * row are computed by the decode kernel and the others by the MFMA prefill
  * kernel: two launches on the stream, told apart on the device (no host
  * synchronisation). */
+/* paged_attention_prefill_wmma over a scaled cache (FP8 E4M3 pools written
+ * by pa_write_kv_scaled): K holds k / k_scale and V holds v / v_scale, so
+ * k_scale joins the softmax scale and v_scale multiplies the output rows.
+ * No reference counterpart (the reference has no FP8 path,
+ * docs/REPORT.md:270); the entry it extends is
+ * kernels/paged_attn_wmma.h:13-15.  Scales must be finite. */
+int paged_attention_prefill_wmma_scaled(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                                        const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                                        const pa_tensor_t* context_lens, double scale, double k_scale,
+                                        double v_scale, void* stream);
+
 int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
                                    const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
                                    const pa_tensor_t* context_lens, const pa_tensor_t* cu_seqlens_q,

@@ -126,7 +126,7 @@ def test_shape_rejections(pa):
 def test_prefill_rejections(pa):
     a = args(pa, prefill=True, kvdt=F32)
     rc, err = call(pa, "paged_attention_prefill_wmma", a, extra=(None,))
-    assert rc == 1 and "fp16 or bf16 KV cache" in err
+    assert rc == 1 and "fp16, bf16 or float8_e4m3fn KV cache" in err
     a = args(pa, prefill=False)
     rc, err = call(pa, "paged_attention_prefill", a, extra=(None,))
     assert rc == 1 and err == "q must be [B, S, H, D]"

@@ -326,7 +326,7 @@ def test_fp8_decode_v3_scaled(pa, dev, D, H, HKV):
 
 
 def test_fp8_unscaled_entry_points(pa, dev):
-    """v1, v2 and the fp32 prefill read an FP8 cache as is (scale 1)."""
+    """v1, v2, the fp32 prefill and the MFMA prefill read an FP8 cache as is (scale 1)."""
     inp, k8, v8, kf, vf = fp8_case(2, 8, 4, 64, 16, [90, 200], seed=5, k_scale=1.0, v_scale=1.0)
     q = torch.from_numpy(inp["q_f32"]).to(dev)
     args = (fp8_dev(k8, dev), fp8_dev(v8, dev), torch.from_numpy(inp["bt"]).to(dev),
@@ -336,8 +336,7 @@ def test_fp8_unscaled_entry_points(pa, dev):
     close(to_host(pa.paged_attention_v2(q, *args, 0.125)), want)
     got = to_host(pa.paged_attention_prefill(q[:, None], *args, 0.125))[:, 0]
     close(got, want)
-    with pytest.raises(RuntimeError, match="the MFMA path needs an fp16 or bf16 KV cache"):
-        pa.paged_attention_prefill_wmma(q[:, None], *args, 0.125)
+    close(to_host(pa.paged_attention_prefill_wmma(q[:, None], *args, 0.125))[:, 0], want)
 
 
 def test_fp8_every_code_through_the_kernel(pa, dev):

@@ -300,3 +300,85 @@ def test_mfma_prefill_plain_and_key_split_modes(pa, dev, kv, qt, D):
         kern = pa.last_launch()
         assert kern.endswith(", true>" if split else ", false>"), kern
         close(to_host(got), want_of(inp, 1.0 / np.sqrt(D)))
+
+
+def fp8_prefill_case(B, S, H, HKV, D, BS, ctx, *, seed, qt, k_scale, v_scale, poison=False):
+    """FP8 E4M3 pool holding K / k_scale and V / v_scale, plus the oracle's
+    inputs: the dequantised values (code * scale) as fp32.  poison: NaN codes
+    (0x7f) in every page slot past a sequence's context and in a spare block
+    that no page references."""
+    inp = prefill_case(B, S, H, HKV, D, BS, ctx, seed=seed, kv="f32", qt=qt)
+    k8 = oracle.fp8_encode(inp["k"] / np.float32(k_scale))
+    v8 = oracle.fp8_encode(inp["v"] / np.float32(v_scale))
+    if poison:
+        k8, v8 = np.concatenate([k8, np.full_like(k8[:1], 0x7F)]), np.concatenate([v8, np.full_like(v8[:1], 0xFF)])
+        for b, c in enumerate(inp["ctx"]):
+            if c > 0 and c % BS:
+                blk = inp["bt"][b, (int(c) - 1) // BS]
+                k8[blk, int(c) % BS:] = 0x7F
+                v8[blk, int(c) % BS:] = 0xFF
+    kf = oracle.fp8_decode(k8) * np.float32(k_scale)
+    vf = oracle.fp8_decode(v8) * np.float32(v_scale)
+    return inp, k8, v8, kf, vf
+
+
+def _fp8(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).view(torch.float8_e4m3fn).to(dev)
+
+
+@pytest.mark.parametrize("qt", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"B{s[0]}S{s[1]}")
+def test_mfma_prefill_fp8(pa, dev, qt, D, shape):
+    """FP8 E4M3 caches on the matrix-core prefill (codes converted exactly to
+    fp16 tiles), unscaled through paged_attention_prefill_wmma and with
+    per-tensor scales through paged_attention_prefill_wmma_scaled, against the
+    oracle on the dequantised cache; q in fp16 (as the tiles) or split hi + lo."""
+    B, S, ctx = shape
+    scale = 1.0 / np.sqrt(D)
+    for ks, vs in ((1.0, 1.0), (0.05, 0.02)):
+        inp, k8, v8, kf, vf = fp8_prefill_case(B, S, 4, 2, D, 16, ctx, seed=D + S + 3, qt=qt, k_scale=ks, v_scale=vs)
+        args = (to_dev(inp["q"], qt, dev), _fp8(k8, dev), _fp8(v8, dev), torch.from_numpy(inp["bt"]).to(dev),
+                torch.from_numpy(inp["ctx"]).to(dev))
+        got = pa.paged_attention_prefill_wmma(*args, scale, k_scale=ks, v_scale=vs)
+        assert "prefill_mfma_kernel<pa::KvFP8" in pa.last_launch(), pa.last_launch()
+        close(to_host(got), oracle.prefill(inp["q_f32"], kf, vf, inp["bt"], inp["ctx"], scale, "f32"))
+
+
+@pytest.mark.parametrize("D,S,ctx,H", [(64, 1024, 1024, 32), (128, 512, 2048, 8)])
+def test_mfma_prefill_fp8_longer_and_poisoned(pa, dev, D, S, ctx, H):
+    """Longer prompts (a plain grid of 512 work-groups and a key-split one)
+    over a scaled FP8 pool whose unattended slots hold NaN codes: every row
+    equals the oracle."""
+    B = 2
+    inp, k8, v8, kf, vf = fp8_prefill_case(B, S, H, 2, D, 16, [ctx - 5, ctx], seed=D, qt="bf16",
+                                           k_scale=1 / 32, v_scale=1 / 24, poison=True)
+    assert not np.isfinite(kf).all()
+    args = (to_dev(inp["q"], "bf16", dev), _fp8(k8, dev), _fp8(v8, dev), torch.from_numpy(inp["bt"]).to(dev),
+            torch.from_numpy(inp["ctx"]).to(dev))
+    scale = 1.0 / np.sqrt(D)
+    got = to_host(pa.paged_attention_prefill_wmma(*args, scale, k_scale=1 / 32, v_scale=1 / 24))
+    assert ("true>" in pa.last_launch()) == (H == 8), pa.last_launch()  # key-split mode for the small grid
+    assert np.isfinite(got).all()
+    close(got, oracle.prefill(inp["q_f32"], kf, vf, inp["bt"], inp["ctx"], scale, "f32"))
+
+
+def test_varlen_fp8(pa, dev):
+    """Mixed decode + prefill batch over an FP8 pool (scale 1): decode rows on
+    the decode kernel, chunks on the FP8 matrix-core prefill."""
+    qlens = [1, 37, 130, 1]
+    ctxs = [700, 37, 1000, 40]
+    H, HKV, D, BS = 4, 2, 128, 16
+    inp, q, q32, cu = varlen_case(qlens, ctxs, H, HKV, D, BS, seed=17, kv="f32", qt="f16")
+    k8, v8 = oracle.fp8_encode(inp["k"]), oracle.fp8_encode(inp["v"])
+    kf, vf = oracle.fp8_decode(k8), oracle.fp8_decode(v8)
+    got = to_host(pa.paged_attention_prefill_varlen(
+        to_dev(q, "f16", dev), _fp8(k8, dev), _fp8(v8, dev), torch.from_numpy(inp["bt"]).to(dev),
+        torch.from_numpy(inp["ctx"]).to(dev), torch.from_numpy(cu).to(dev), max(qlens), 1.0 / np.sqrt(D)))
+    launched = pa.last_launch()
+    assert "decode_kernel" in launched and "prefill_mfma_kernel<pa::KvFP8" in launched, launched
+    for b in range(len(qlens)):
+        rows = slice(cu[b], cu[b + 1])
+        want = oracle.prefill(q32[rows][None], kf, vf, inp["bt"][b:b + 1], inp["ctx"][b:b + 1], 1.0 / np.sqrt(D),
+                              "f32")[0]
+        close(got[rows], want)

@@ -83,6 +83,19 @@ def test_write_kv_scaled_op(pa, dev):
     assert np.array_equal(vc.view(torch.uint8).cpu().numpy(), wv)
 
 
+def test_prefill_wmma_scaled_op(pa, dev):
+    """torch.ops.gb10_attn.paged_attention_prefill_wmma_scaled over an FP8 pool equals the Python mirror."""
+    ops = pa.torch_ops()
+    inp = decode_case(2, 4, 2, 64, 16, [70, 130], seed=41, kv="f32")
+    k8 = torch.from_numpy(oracle.fp8_encode(inp["k"] / np.float32(0.05))).view(torch.float8_e4m3fn).to(dev)
+    v8 = torch.from_numpy(oracle.fp8_encode(inp["v"] / np.float32(0.03))).view(torch.float8_e4m3fn).to(dev)
+    q = torch.randn(2, 40, 4, 64, generator=torch.Generator().manual_seed(41)).to(dev)
+    bt, ctx = torch.from_numpy(inp["bt"]).to(dev), torch.from_numpy(inp["ctx"]).to(dev)
+    got = ops.paged_attention_prefill_wmma_scaled(q, k8, v8, bt, ctx, 0.125, 0.05, 0.03)
+    want = pa.paged_attention_prefill_wmma(q, k8, v8, bt, ctx, 0.125, k_scale=0.05, v_scale=0.03)
+    assert got.dtype == torch.float32 and torch.equal(got, want)
+
+
 def test_reference_error_messages(pa, dev):
     ops = pa.torch_ops()
     inp = decode_case(1, 8, 4, 64, 16, [20], seed=36)
@@ -91,7 +104,7 @@ def test_reference_error_messages(pa, dev):
         ops.paged_attention_v3(q[:, :6].contiguous(), k, v, bt, ctx, 0.1, 0)
     inp = decode_case(1, 4, 4, 64, 16, [20], seed=36, kv="f32")
     q, k, v, bt, ctx = dev_inputs(inp, dev)
-    with pytest.raises(RuntimeError, match="the MFMA path needs an fp16 or bf16 KV cache"):
+    with pytest.raises(RuntimeError, match="the MFMA path needs an fp16, bf16 or float8_e4m3fn KV cache"):
         ops.paged_attention_prefill_wmma(q[:, None], k, v, bt, ctx, 0.1)
 
 
