@@ -841,6 +841,8 @@ int pa_write_kv_scaled(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tens
   p.src_dtype = sd; p.cache_dtype = cd; p.slot_i64 = slot_mapping->dtype == kI64;
   p.k_scale = (float)k_scale; p.v_scale = (float)v_scale;
   p.k_rcp = 1.0f / p.k_scale; p.v_rcp = 1.0f / p.v_scale;  // IEEE single division: correctly rounded
+  auto in_range = [](float r) { return std::fabs(r) >= 0x1p-60f && std::fabs(r) <= 0x1p60f; };
+  p.k_fast = in_range(p.k_rcp); p.v_fast = in_range(p.v_rcp);
   p.unit_scale = p.k_scale == 1.0f && p.v_scale == 1.0f;
   p.bs_div = make_fastdiv((uint32_t)BS);
   return hip_status(launch_write_kv(p, static_cast<hipStream_t>(stream)), "KV write kernel launch");

@@ -126,6 +126,7 @@ struct WriteParams {
   int32_t unit_scale;  // 1: k_scale == v_scale == 1 (no division)
   float k_scale, v_scale;  // the cache holds key / k_scale and value / v_scale
   float k_rcp, v_rcp;      // 1 / k_scale, 1 / v_scale rounded to nearest (fp32)
+  int32_t k_fast, v_fast;  // |k_rcp|, |v_rcp| in [2^-60, 2^60]: the reciprocal-based division applies
   FastDiv bs_div;
 };
 

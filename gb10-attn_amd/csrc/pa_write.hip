@@ -67,14 +67,15 @@ __device__ inline uint32_t fp8_e4m3_code(float x) {
 
 // x / s rounded to nearest, from r = RN(1 / s): q = RN(x r) is within one ulp
 // of x / s, the residual x - q s is exact in one FMA, and RN(q + (x - q s) r)
-// is the correctly rounded quotient (Markstein's theorem) while no
-// intermediate leaves the normal range; outside it (and for zero, NaN,
-// infinities) the full-precision division is taken.
-__device__ inline float div_rn(float x, float s, float r) {
+// is the correctly rounded quotient (Markstein's theorem) while x, r and q
+// stay in the normal range.  fast: |r| in [2^-60, 2^60] (host-checked); then
+// |x| in [2^-60, 2^61) keeps q normal.  Otherwise (zero, subnormal, huge,
+// NaN, infinite operands) the full-precision division is taken.
+__device__ inline float div_rn(float x, float s, float r, bool fast) {
   const float q = x * r;
-  const float aq = __builtin_fabsf(q);
-  if (!(aq >= 0x1p-100f && aq <= 0x1p100f)) return (x == 0.0f || x != x) ? q : __fdiv_rn(x, s);
-  return __builtin_fmaf(__builtin_fmaf(-q, s, x), r, q);
+  const uint32_t e = (__builtin_bit_cast(uint32_t, x) >> 23) & 0xffu;  // biased exponent of x
+  if (fast && e - 67u <= 120u) return __builtin_fmaf(__builtin_fmaf(-q, s, x), r, q);
+  return (x == 0.0f || x != x) ? q : __fdiv_rn(x, s);
 }
 
 template <int DST>
@@ -157,13 +158,13 @@ __global__ __launch_bounds__(kWriteThreads) void write_kv_kernel(const WritePara
   load8<SRC>(p.key, ks, x);
   if (!p.unit_scale) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = div_rn(x[e], p.k_scale, p.k_rcp);
+    for (int e = 0; e < 8; ++e) x[e] = div_rn(x[e], p.k_scale, p.k_rcp, p.k_fast);
   }
   store8<DST>(p.kc, kd, x);
   load8<SRC>(p.value, vs, x);
   if (!p.unit_scale) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = div_rn(x[e], p.v_scale, p.v_rcp);
+    for (int e = 0; e < 8; ++e) x[e] = div_rn(x[e], p.v_scale, p.v_rcp, p.v_fast);
   }
   store8<DST>(p.vc, vd, x);
 }
