@@ -27,7 +27,7 @@ EXPORTS = (
     "pa_v3_partition", "pa_v3_reduce",
     "choose_num_splits", "choose_num_splits_for", "pa_plan_partitions",
     "paged_attention_prefill", "paged_attention_prefill_wmma", "paged_attention_prefill_wmma_scaled",
-    "paged_attention_prefill_varlen",
+    "paged_attention_prefill_varlen", "paged_attention_prefill_varlen_scaled",
     "pa_write_kv", "pa_write_kv_scaled",
 )
 
@@ -102,6 +102,8 @@ def lib() -> C.CDLL:
     L.paged_attention_prefill_wmma_scaled.argtypes = six + [C.c_double, C.c_double, C.c_double, P]
     L.paged_attention_prefill_varlen.restype = C.c_int
     L.paged_attention_prefill_varlen.argtypes = six + [T, i64, C.c_double, P]
+    L.paged_attention_prefill_varlen_scaled.restype = C.c_int
+    L.paged_attention_prefill_varlen_scaled.argtypes = six + [T, i64, C.c_double, C.c_double, C.c_double, P]
     L.pa_write_kv.restype = C.c_int
     L.pa_write_kv.argtypes = [T, T, T, T, T, P]
     L.pa_write_kv_scaled.restype = C.c_int

@@ -708,7 +708,18 @@ int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const
                                    const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
                                    const pa_tensor_t* context_lens, const pa_tensor_t* cu_seqlens_q,
                                    int64_t max_q_len, double scale, void* stream) {
+  return paged_attention_prefill_varlen_scaled(out, q, k_cache, v_cache, block_tables, context_lens, cu_seqlens_q,
+                                               max_q_len, scale, 1.0, 1.0, stream);
+}
+
+int paged_attention_prefill_varlen_scaled(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                                          const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                                          const pa_tensor_t* context_lens, const pa_tensor_t* cu_seqlens_q,
+                                          int64_t max_q_len, double scale, double k_scale, double v_scale,
+                                          void* stream) {
   int rc;
+  if (!std::isfinite(k_scale) || !std::isfinite(v_scale))
+    return fail(PA_ERR_INVALID_ARGUMENT, "k_scale and v_scale must be finite");
   if ((rc = check_tensor(q, "q", 3, "[T, H, D]"))) return rc;
   if ((rc = check_tensor(out, "out", 3, "[T, H, D]"))) return rc;
   if ((rc = check_tensor(block_tables, "block_tables", 2, "[B, MB]"))) return rc;
@@ -732,7 +743,7 @@ int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const
   o4.data = out->data;
   o4.dtype = out->dtype;
   DecodeArgs a;
-  rc = check_args(&o4, &q4, k_cache, v_cache, block_tables, context_lens, scale, true, &a);
+  rc = check_args(&o4, &q4, k_cache, v_cache, block_tables, context_lens, scale * k_scale, true, &a);
   if (rc) return rc;
   if (max_q_len == 0 || T == 0) return PA_OK;
   g_launches.clear();
@@ -744,7 +755,8 @@ int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const
   const bool prefill_ok = (a.kv_dtype == kF16 || a.kv_dtype == kBF16 || a.kv_dtype == kFP8) && a.p.D <= 256 &&
                           (reinterpret_cast<uintptr_t>(q->data) & 15) == 0 && (int64_t)a.p.B * a.p.H > 0;
   if (prefill_ok) {  // (otherwise the prefill call below reports why, before any launch)
-    DecodeArgs d = a;
+    DecodeArgs d = a;  // check_args folded k_scale into d.p.qscale
+    d.p.vscale = (float)v_scale;
     d.p.Sq = 1;
     d.p.cu_q = cu;
     d.p.q_total = T;
@@ -758,7 +770,7 @@ int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const
                          "decode kernel launch")))
       return rc;
   }
-  return run_prefill_mfma(a, q, cu, T, scale, stream, true);
+  return run_prefill_mfma(a, q, cu, T, scale * k_scale, stream, true, v_scale);
 }
 
 int pa_write_kv(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tensor_t* key,

@@ -170,17 +170,25 @@ at::Tensor op_paged_attention_v3_scaled(const at::Tensor& q, const at::Tensor& k
   return out;
 }
 
-at::Tensor op_paged_attention_prefill_varlen(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
-                                             const at::Tensor& bt, const at::Tensor& ctx, const at::Tensor& cu,
-                                             int64_t max_q_len, double scale) {
+at::Tensor op_paged_attention_prefill_varlen_scaled(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                                    const at::Tensor& bt, const at::Tensor& ctx, const at::Tensor& cu,
+                                                    int64_t max_q_len, double scale, double k_scale,
+                                                    double v_scale) {
   Args a = prep(q, k, v, bt, ctx, 3, "[T, H, D]");
   at::Tensor cuq = cu.to(a.q.device(), at::kInt).contiguous();
   c10::DeviceGuard guard(a.q.device());
   at::Tensor out = at::empty(a.q.sizes(), a.q.options().dtype(at::kFloat));
   pa_tensor_t o = view(out), qq = view(a.q), kk = view(a.k), vv = view(a.v), bb = view(a.bt), cc = view(a.ctx),
               uu = view(cuq);
-  check(paged_attention_prefill_varlen(&o, &qq, &kk, &vv, &bb, &cc, &uu, max_q_len, scale, stream_of(a.q)));
+  check(paged_attention_prefill_varlen_scaled(&o, &qq, &kk, &vv, &bb, &cc, &uu, max_q_len, scale, k_scale, v_scale,
+                                              stream_of(a.q)));
   return out;
+}
+
+at::Tensor op_paged_attention_prefill_varlen(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                             const at::Tensor& bt, const at::Tensor& ctx, const at::Tensor& cu,
+                                             int64_t max_q_len, double scale) {
+  return op_paged_attention_prefill_varlen_scaled(q, k, v, bt, ctx, cu, max_q_len, scale, 1.0, 1.0);
 }
 
 int64_t op_choose_num_splits(int64_t num_seqs, int64_t num_heads, int64_t max_context) {
@@ -232,6 +240,9 @@ TORCH_LIBRARY(gb10_attn, m) {
   m.def("paged_attention_prefill_varlen(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, "
         "Tensor context_lens, Tensor cu_seqlens_q, int max_q_len, float scale) -> Tensor",
         &op_paged_attention_prefill_varlen);
+  m.def("paged_attention_prefill_varlen_scaled(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables, "
+        "Tensor context_lens, Tensor cu_seqlens_q, int max_q_len, float scale, float k_scale, float v_scale) -> Tensor",
+        &op_paged_attention_prefill_varlen_scaled);
   m.def("write_kv(Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor key, Tensor value, Tensor slot_mapping) -> ()",
         &op_write_kv);
   m.def("write_kv_scaled(Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor key, Tensor value, Tensor slot_mapping, "

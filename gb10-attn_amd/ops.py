@@ -131,19 +131,21 @@ def paged_attention_prefill_wmma(q, k_cache, v_cache, block_tables, context_lens
 
 
 def paged_attention_prefill_varlen(q, k_cache, v_cache, block_tables, context_lens, cu_seqlens_q,
-                                   max_q_len, scale, *, out_dtype=torch.float32, out=None):
+                                   max_q_len, scale, *, out_dtype=torch.float32, out=None, k_scale=1.0,
+                                   v_scale=1.0):
     """Mixed decode + prefill batch on the MFMA path: q/out packed [T, H, D],
     sequence b's q_len_b = cu_seqlens_q[b+1] - cu_seqlens_q[b] new tokens at
-    rows cu_seqlens_q[b] .., positions context_lens[b] - q_len_b + r (causal)."""
+    rows cu_seqlens_q[b] .., positions context_lens[b] - q_len_b + r (causal).
+    k_scale / v_scale dequantise a scaled cache (paged_attention_prefill_varlen_scaled)."""
     q, k_cache, v_cache, block_tables, context_lens = _prep(
         q, k_cache, v_cache, block_tables, context_lens, 3, "[T, H, D]")
     cu = cu_seqlens_q.to(q.device, torch.int32).contiguous()
     o = _out(q, out_dtype, out)
     with torch.cuda.device(q.device):
-        check(lib().paged_attention_prefill_varlen(
+        check(lib().paged_attention_prefill_varlen_scaled(
             C.byref(view(o)), C.byref(view(q)), C.byref(view(k_cache)), C.byref(view(v_cache)),
             C.byref(view(block_tables)), C.byref(view(context_lens)), C.byref(view(cu)), int(max_q_len),
-            float(scale), _stream(q.device)))
+            float(scale), float(k_scale), float(v_scale), _stream(q.device)))
     return o
 
 

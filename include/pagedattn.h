@@ -244,6 +244,17 @@ int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const
                                    const pa_tensor_t* context_lens, const pa_tensor_t* cu_seqlens_q,
                                    int64_t max_q_len, double scale, void* stream);
 
+/* paged_attention_prefill_varlen over a scaled cache (FP8 E4M3 pools written
+ * by pa_write_kv_scaled): k_scale joins the softmax scale and v_scale
+ * multiplies the output rows, in both kernels of the call.  No reference
+ * counterpart (the reference has no FP8 path, docs/REPORT.md:270).  Scales
+ * must be finite. */
+int paged_attention_prefill_varlen_scaled(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                                          const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                                          const pa_tensor_t* context_lens, const pa_tensor_t* cu_seqlens_q,
+                                          int64_t max_q_len, double scale, double k_scale, double v_scale,
+                                          void* stream);
+
 /* KV-cache write ("reshape and cache"): token t's K and V rows, key[t] and
  * value[t] ([T, HKV, D], any non-negative token/head strides, 16-byte aligned
  * rows), go to block slot_mapping[t] / BS, row slot_mapping[t] % BS of

@@ -363,18 +363,21 @@ def test_mfma_prefill_fp8_longer_and_poisoned(pa, dev, D, S, ctx, H):
     close(got, oracle.prefill(inp["q_f32"], kf, vf, inp["bt"], inp["ctx"], scale, "f32"))
 
 
-def test_varlen_fp8(pa, dev):
-    """Mixed decode + prefill batch over an FP8 pool (scale 1): decode rows on
-    the decode kernel, chunks on the FP8 matrix-core prefill."""
+@pytest.mark.parametrize("ks,vs,qt", [(1.0, 1.0, "f16"), (0.04, 0.03, "bf16")])
+def test_varlen_fp8(pa, dev, ks, vs, qt):
+    """Mixed decode + prefill batch over an FP8 pool, unscaled and through
+    paged_attention_prefill_varlen_scaled: decode rows on the decode kernel,
+    chunks on the FP8 matrix-core prefill."""
     qlens = [1, 37, 130, 1]
     ctxs = [700, 37, 1000, 40]
     H, HKV, D, BS = 4, 2, 128, 16
-    inp, q, q32, cu = varlen_case(qlens, ctxs, H, HKV, D, BS, seed=17, kv="f32", qt="f16")
-    k8, v8 = oracle.fp8_encode(inp["k"]), oracle.fp8_encode(inp["v"])
-    kf, vf = oracle.fp8_decode(k8), oracle.fp8_decode(v8)
+    inp, q, q32, cu = varlen_case(qlens, ctxs, H, HKV, D, BS, seed=17, kv="f32", qt=qt)
+    k8, v8 = oracle.fp8_encode(inp["k"] / np.float32(ks)), oracle.fp8_encode(inp["v"] / np.float32(vs))
+    kf, vf = oracle.fp8_decode(k8) * np.float32(ks), oracle.fp8_decode(v8) * np.float32(vs)
     got = to_host(pa.paged_attention_prefill_varlen(
-        to_dev(q, "f16", dev), _fp8(k8, dev), _fp8(v8, dev), torch.from_numpy(inp["bt"]).to(dev),
-        torch.from_numpy(inp["ctx"]).to(dev), torch.from_numpy(cu).to(dev), max(qlens), 1.0 / np.sqrt(D)))
+        to_dev(q, qt, dev), _fp8(k8, dev), _fp8(v8, dev), torch.from_numpy(inp["bt"]).to(dev),
+        torch.from_numpy(inp["ctx"]).to(dev), torch.from_numpy(cu).to(dev), max(qlens), 1.0 / np.sqrt(D),
+        k_scale=ks, v_scale=vs))
     launched = pa.last_launch()
     assert "decode_kernel" in launched and "prefill_mfma_kernel<pa::KvFP8" in launched, launched
     for b in range(len(qlens)):
