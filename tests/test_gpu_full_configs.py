@@ -10,6 +10,8 @@ and check what the oracle can afford there:
   * config 3 (B=32, 32 query / 8 KV heads, D=128, bf16, ragged contexts in
     [1024, 32768]): every sequence against the oracle; block permutation
     invariance bit for bit;
+  * config 3 over an FP8 E4M3 pool written by the scaled KV write: every
+    sequence against the oracle on the dequantised pool;
   * configs 4a / 4b (causal prefill): query rows against the oracle's decode
     of the row's prefix (a prefill row is the decode of its prefix, which
     tests/test_oracle.py pins) -- every row of 4a, and at 4b every 16th row
@@ -114,6 +116,34 @@ def test_config3_full(pa, dev):
     k2, v2, bt2 = permuted(k, v, bt, 33)
     got2 = pa.paged_attention_v3(q, k2, v2, bt2, cl, scale, 0, out_dtype=torch.bfloat16)
     assert torch.equal(got16, got2), "block permutation changed the output"
+
+
+def test_config3_fp8_full(pa, dev):
+    """Config 3 over an FP8 E4M3 pool: bf16 K/V quantised by pa_write_kv_scaled
+    (scale 1/16), decoded by the scaled v3 path; every sequence against the
+    oracle on the dequantised pool."""
+    B, H, HKV, D, BS = 32, 32, 8, 128, 16
+    ks = vs = 1.0 / 16
+    ctx = np.random.default_rng(3).integers(1024, 32769, B).astype(np.int32)
+    g = torch.Generator(device=dev)
+    g.manual_seed(34)
+    bt_np, nb = ragged_tables(ctx, BS, 35)
+    k8 = torch.zeros((nb, BS, HKV, D), dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    v8 = torch.zeros_like(k8)
+    for part in torch.arange(nb, device=dev).chunk(8):  # the pool written in slices (bounded source size)
+        n = part.numel()
+        slots = (part[:, None] * BS + torch.arange(BS, device=dev)).reshape(-1)
+        pa.write_kv(k8, v8, randn((n * BS, HKV, D), g, dev, torch.bfloat16),
+                    randn((n * BS, HKV, D), g, dev, torch.bfloat16), slots, k_scale=ks, v_scale=vs)
+    q = randn((B, H, D), g, dev, torch.bfloat16)
+    bt = torch.from_numpy(bt_np).to(dev)
+    cl = torch.from_numpy(ctx).to(dev)
+    scale = 1.0 / np.sqrt(D)
+    got = pa.paged_attention_v3(q, k8, v8, bt, cl, scale, 0, out_dtype=torch.float32, k_scale=ks, v_scale=vs)
+    kf = oracle.fp8_decode(k8.view(torch.uint8).cpu().numpy()) * np.float32(ks)
+    vf = oracle.fp8_decode(v8.view(torch.uint8).cpu().numpy()) * np.float32(vs)
+    want = oracle_decode_rows(q.float().cpu().numpy(), kf, vf, bt_np, ctx, scale, "f32", 1)
+    close(to_host(got), want)
 
 
 PREFILL = {  # name: (B, S, H, D, dtype, rows checked)
