@@ -62,11 +62,46 @@
 #ifndef PA_DECODE_PPRIO
 #define PA_DECODE_PPRIO 1  // one-head work-groups of a fully resident grid: priority falls with progress
 #endif
+#ifndef PA_DECODE_COMPACT
+#define PA_DECODE_COMPACT 1  // ragged batches: the work-groups a sequence needs first, the idle ones last
+#endif
 #ifndef PA_DECODE_MFMA
 #define PA_DECODE_MFMA 1  // GQA groups of >= 4 heads on the matrix-core kernel
 #endif
 
 namespace pa {
+
+// Ragged batches with fixed-length partitions: the grid holds `parts`
+// partitions per (sequence, head unit), sized for the longest context a
+// block-table row can hold, but a sequence of ctx tokens needs only
+// ceil(ctx / part_tokens) of them (one for an empty or invalid row, which
+// writes its fill).  In plain numbering the idle work-groups are spread
+// through the grid and each holds a dispatch slot for a context-length load;
+// compacted numbering gives the needed units the first ids, sequence by
+// sequence (heads fastest, as before), and the idle ones the last.  Every
+// wave derives the numbering from the context lengths itself: one load per
+// lane and a prefix sum across the wave, hence at most 64 sequences.
+__device__ inline bool compact_grid(const DecodeParams& p) {
+  return PA_DECODE_COMPACT && p.part_tokens > 0 && p.Sq == 1 && p.B <= 64 && p.cu_q == nullptr;
+}
+// Unit `id` of the compacted numbering -> (z, part); false past the last one.
+__device__ inline bool compact_unit(const DecodeParams& p, int id, int lane, int& z, int& part) {
+  const int maxctx = p.MB * p.BS;
+  const int c = lane < p.B ? p.context_lens[lane] : 0;
+  const int np = lane < p.B ? (c > 0 && c <= maxctx ? (c - 1) / p.part_tokens + 1 : 1) : 0;
+  int incl = np;  // inclusive prefix sum of the units over sequences 0..lane
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o, 64);
+    incl += lane >= o ? t : 0;
+  }
+  // Sequences whose units all precede id form a prefix of the lanes.
+  const int zz = __builtin_popcountll(__builtin_amdgcn_ballot_w64(incl <= id));
+  if (zz >= p.B) return false;
+  z = zz;
+  part = id - __builtin_amdgcn_readlane(incl - np, zz);
+  return true;
+}
 
 template <typename KV, int D, int NIO = 0>
 struct DecodeShape {
@@ -159,8 +194,13 @@ void decode_kernel(const DecodeParams p) {
   int id = blockIdx.x;
   int y = id % units_y;
   id /= units_y;
-  const int part = id % p.parts;
-  const int z = id / p.parts;
+  int part, z;
+  if (compact_grid(p)) {
+    if (!compact_unit(p, id, lane, z, part)) return;  // work-group uniform
+  } else {
+    part = id % p.parts;
+    z = id / p.parts;
+  }
   // One head per work-group (MHA, unpacked): rotate the head order by the
   // (sequence, partition) index.  Work-groups reach the 8 XCDs round robin,
   // so without it an XCD keeps reading the same few 128-byte head slices of
@@ -350,9 +390,16 @@ void decode_kernel(const DecodeParams p) {
         KV::template to_pairs<DQ>(T.k[i], kp);
 #pragma unroll
         for (int g = 0; g < GC; ++g) {
-          d[g] = 0.0f;
+          // GQA groups start each chain from the three-operand form (no zero
+          // move: FP8 config 3 +3 %); one-head work-groups, bound by HBM
+          // rather than vector issue, keep the builtin's code.
+          if constexpr (GC > 1) {
+            d[g] = dot2_first<DQ>(qp[g][0], kp[0]);
+          } else {
+            d[g] = dot2<DQ>(qp[g][0], kp[0], 0.0f);
+          }
 #pragma unroll
-          for (int w = 0; w < VEC / 2; ++w) d[g] = dot2<DQ>(qp[g][w], kp[w], d[g]);
+          for (int w = 1; w < VEC / 2; ++w) d[g] = dot2<DQ>(qp[g][w], kp[w], d[g]);
         }
       } else {
         float kf[VEC];
@@ -431,7 +478,7 @@ void decode_kernel(const DecodeParams p) {
       mx_own = fmaxf(mx_own, mt);
       const bool up = mt > m_own + 8.0f;
       if (__builtin_amdgcn_ballot_w64(up) != 0) {
-        const float mtg[4] = {dpp<0x00>(mt), dpp<0x55>(mt), dpp<0xAA>(mt), dpp<0xFF>(mt)};
+        const float mtg[4] = {dpp_quad<0x00>(mt), dpp_quad<0x55>(mt), dpp_quad<0xAA>(mt), dpp_quad<0xFF>(mt)};
 #pragma unroll
         for (int g = 0; g < GC; ++g) {
           const float mn = mtg[g] > m[g] + 8.0f ? mtg[g] : m[g];
@@ -446,10 +493,10 @@ void decode_kernel(const DecodeParams p) {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const float pl = ((T.live >> i) & 1u) ? fast_exp2(so[i] - m_own) : 0.0f;
-        pw[i][0] = dpp<0x00>(pl);
-        pw[i][1] = dpp<0x55>(pl);
-        pw[i][2] = dpp<0xAA>(pl);
-        pw[i][3] = dpp<0xFF>(pl);
+        pw[i][0] = dpp_quad<0x00>(pl);
+        pw[i][1] = dpp_quad<0x55>(pl);
+        pw[i][2] = dpp_quad<0xAA>(pl);
+        pw[i][3] = dpp_quad<0xFF>(pl);
       }
     } else {
       // Lazy rescale: a stream's reference point m is raised only when a tile
@@ -575,10 +622,10 @@ void decode_kernel(const DecodeParams p) {
   // (the partials carry the maximum, kernels/paged_attn_v3.cu:113-122).
   if constexpr (LAZY) {
     if constexpr (PBC) {  // the heads' maxima live in the quad's lanes
-      mx[0] = dpp<0x00>(mx_own);
-      mx[1] = dpp<0x55>(mx_own);
-      mx[2] = dpp<0xAA>(mx_own);
-      mx[3] = dpp<0xFF>(mx_own);
+      mx[0] = dpp_quad<0x00>(mx_own);
+      mx[1] = dpp_quad<0x55>(mx_own);
+      mx[2] = dpp_quad<0xAA>(mx_own);
+      mx[3] = dpp_quad<0xFF>(mx_own);
     }
 #pragma unroll
     for (int g = 0; g < GC; ++g) {

@@ -120,8 +120,13 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(const DecodeParams p) 
   int id = blockIdx.x;
   const int y = id % units_y;
   id /= units_y;
-  const int part = id % p.parts;
-  const int z = id / p.parts;
+  int part, z;
+  if (compact_grid(p)) {
+    if (!compact_unit(p, id, lane, z, part)) return;  // work-group uniform
+  } else {
+    part = id % p.parts;
+    z = id / p.parts;
+  }
   const int kvh = y / p.head_chunks;
   const int hc = y - kvh * p.head_chunks;
   const int b = z / p.Sq;

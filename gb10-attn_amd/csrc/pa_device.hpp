@@ -139,6 +139,26 @@ __device__ inline float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
                                           false);
 }
+// The first product of a chain: a.lo * b.lo + a.hi * b.hi from a zero
+// accumulator.  Through the builtin the compiler materialises the zero with a
+// v_mov_b32 and then uses the accumulating v_dot2c form; the three-operand
+// form takes the zero as an inline constant.
+#ifndef PA_DOT2_FIRST_ASM
+#define PA_DOT2_FIRST_ASM 1
+#endif
+template <int PT>
+__device__ inline float dot2_first(uint32_t a, uint32_t b) {
+  if constexpr (PA_DOT2_FIRST_ASM) {
+    float r;
+    if constexpr (PT == kF16)
+      asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    else
+      asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+  } else {
+    return dot2<PT>(a, b, 0.0f);
+  }
+}
 template <int PT>
 __device__ inline uint32_t pack_pair_exact(float x, float y) {
   if constexpr (PT == kF16)
@@ -286,6 +306,22 @@ template <int CTRL>
 __device__ inline float dpp(float v) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+// A quad permutation as a plain move (a broadcast whose result feeds no
+// add): every lane reads a lane of its own quad, so the value a lane would
+// keep without a source is never needed, and the mov form leaves it
+// undefined instead of materialising a zero (one v_mov_b32 per use).  dpp()
+// keeps the zero: the compiler folds that form into a following add.
+#ifndef PA_DPP_MOV
+#define PA_DPP_MOV 1
+#endif
+template <int CTRL>
+__device__ inline float dpp_quad(float v) {
+  static_assert(CTRL >= 0 && CTRL <= 0xff, "quad permutations only");
+  if constexpr (PA_DPP_MOV)
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+  else
+    return dpp<CTRL>(v);
 }
 
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
