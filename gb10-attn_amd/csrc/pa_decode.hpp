@@ -158,6 +158,8 @@ void decode_kernel(const DecodeParams p) {
   // Groups of four heads whose KV head's row spans one 16-lane DPP row: each
   // lane of a quad finishes one head's score (transposing reduction) and its
   // exponential, shared across the quad.
+  // The lane keeps its own head's row sum, shared across the quad once at the
+  // end; with packed P.V the own weights are packed before they are shared.
   constexpr bool PBC = PA_DECODE_PBCAST && LAZY && GC == 4 && D / VEC == 16;
   constexpr bool PVP = PA_DECODE_PVDOT && LAZY && (Sh::NI % 2 == 0) && KV::kCode != kBF16 &&
                        ((pair_types<KV>::value >> kF16) & 1);
@@ -257,17 +259,23 @@ void decode_kernel(const DecodeParams p) {
   }
 
   // This lane's slice of q for the GC heads, pre-scaled into log2 units.
+  // PBC: lane j of each quad holds the heads in the order j, j^1, j^2, j^3
+  // (slot g holds head g ^ j), so the transposing reduction below needs no
+  // selects: at each exchange step the value a lane keeps and the value its
+  // partner needs sit in fixed slots.
   float qr[GC][VEC];
+  const int qperm = PBC ? (lane & 3) : 0;
 #pragma unroll
   for (int g = 0; g < GC; ++g) {
-    const bool hv = g0 + g < p.G;
-    const int h = (kvh * HP + hl) * p.G + g0 + (hv ? g : 0);
+    const int gq = g ^ qperm;
+    const bool hv = g0 + gq < p.G;
+    const int h = (kvh * HP + hl) * p.G + g0 + (hv ? gq : 0);
     const int64_t qb = (zq * p.H + h) * D + dsub * VEC;
     load_elems<VEC>(p.q, p.q_dtype, qb, qr[g]);
   }
 #pragma unroll
   for (int g = 0; g < GC; ++g) {
-    const bool hv = g0 + g < p.G;
+    const bool hv = g0 + (g ^ qperm) < p.G;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) qr[g][e] = hv ? (DQ ? qr[g][e] : qr[g][e] * p.qscale) : 0.0f;
   }
@@ -281,6 +289,7 @@ void decode_kernel(const DecodeParams p) {
 
   float m[GC], l[GC], acc[GC][VEC], mx[GC];
   float m_own = kNegBig, mx_own = kNegBig;  // PBC: this lane's head's reference point and true maximum
+  float l_own = 0.0f;                       // PBC: this lane's head's row sum
 #pragma unroll
   for (int g = 0; g < GC; ++g) {
     m[g] = kNegBig;
@@ -416,14 +425,12 @@ void decode_kernel(const DecodeParams p) {
         // Transposing sum over the 16-lane slot: after the two quad steps
         // lane j of each quad holds head j's sum over the quad, then the
         // four quads are added (row rotations by 4 and 8).
-        const bool b0 = (lane & 1) != 0, b1 = (lane & 2) != 0;
-        float k0 = b0 ? d[1] : d[0], k1 = b0 ? d[3] : d[2];
-        const float t0 = b0 ? d[0] : d[1], t1 = b0 ? d[2] : d[3];
-        k0 += dpp<kDppXor1>(t0);
-        k1 += dpp<kDppXor1>(t1);
-        float k = b1 ? k1 : k0;
-        const float t = b1 ? k0 : k1;
-        k += dpp<kDppXor2>(t);
+        // Slots hold heads j, j^1, j^2, j^3 (j = lane % 4): the xor-1
+        // partner's slots 1 and 3 are this lane's heads j and j^2, and the
+        // xor-2 partner's k1 is head j.
+        const float k0 = d[0] + dpp<kDppXor1>(d[1]);
+        const float k1 = d[2] + dpp<kDppXor1>(d[3]);
+        float k = k0 + dpp<kDppXor2>(k1);
         // Rotation by 8 first: quad q then holds (P_q + P_q+2) + (P_q+1 + P_q+3)
         // in an order that differs between quads only by commuting operands,
         // so all four quads hold bitwise-identical sums.
@@ -469,6 +476,7 @@ void decode_kernel(const DecodeParams p) {
       for (int i = 0; i < NI; ++i) KV::widen(vr[i], vf[i]);
     }
     float pw[NI][GC];  // weights 2^(s - m) of each token and head
+    uint32_t wp[PBC && PVP ? NI / 2 : 1][GC];  // PBC with packed P.V: the weights as fp16 pairs of two tokens
     if constexpr (PBC) {
       // The lane's own head: its tile maximum, the lazy test against its
       // reference point, and one exponential per token, shared across the quad.
@@ -483,20 +491,38 @@ void decode_kernel(const DecodeParams p) {
         for (int g = 0; g < GC; ++g) {
           const float mn = mtg[g] > m[g] + 8.0f ? mtg[g] : m[g];
           const float corr = fast_exp2(m[g] - mn);
-          l[g] *= corr;
 #pragma unroll
           for (int e = 0; e < VEC; ++e) acc[g][e] *= corr;
           m[g] = mn;
         }
+        l_own *= fast_exp2(m_own - (up ? mt : m_own));
         m_own = up ? mt : m_own;
       }
+      float pl[NI];
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        const float pl = ((T.live >> i) & 1u) ? fast_exp2(so[i] - m_own) : 0.0f;
-        pw[i][0] = dpp_quad<0x00>(pl);
-        pw[i][1] = dpp_quad<0x55>(pl);
-        pw[i][2] = dpp_quad<0xAA>(pl);
-        pw[i][3] = dpp_quad<0xFF>(pl);
+      for (int i = 0; i < NI; ++i) pl[i] = ((T.live >> i) & 1u) ? fast_exp2(so[i] - m_own) : 0.0f;
+      if constexpr (PVP) {
+        // The lane's own head: two tokens' weights as one fp16 pair, its row
+        // sum over the rounded pair, and the pairs shared across the quad.
+#pragma unroll
+        for (int u = 0; u < NI / 2; ++u) {
+          const uint32_t own =
+              __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{pl[2 * u], pl[2 * u + 1]}, f16x2_t));
+          l_own = dot2<kF16>(own, 0x3c003c00u, l_own);
+          wp[u][0] = dpp_quad_u<0x00>(own);
+          wp[u][1] = dpp_quad_u<0x55>(own);
+          wp[u][2] = dpp_quad_u<0xAA>(own);
+          wp[u][3] = dpp_quad_u<0xFF>(own);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          l_own += pl[i];
+          pw[i][0] = dpp_quad<0x00>(pl[i]);
+          pw[i][1] = dpp_quad<0x55>(pl[i]);
+          pw[i][2] = dpp_quad<0xAA>(pl[i]);
+          pw[i][3] = dpp_quad<0xFF>(pl[i]);
+        }
       }
     } else {
       // Lazy rescale: a stream's reference point m is raised only when a tile
@@ -542,10 +568,15 @@ void decode_kernel(const DecodeParams p) {
         // then one packed dot product per element: acc[e] += p0 v0[e] + p1 v1[e].
 #pragma unroll
         for (int u = 0; u < NI / 2; ++u) {
-          const float p0 = pw[2 * u][g];
-          const float p1 = pw[2 * u + 1][g];
-          const uint32_t pp = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{p0, p1}, f16x2_t));
-          lg = dot2<kF16>(pp, 0x3c003c00u, lg);
+          uint32_t pp;
+          if constexpr (PBC) {
+            pp = wp[u][g];
+          } else {
+            const float p0 = pw[2 * u][g];
+            const float p1 = pw[2 * u + 1][g];
+            pp = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{p0, p1}, f16x2_t));
+            lg = dot2<kF16>(pp, 0x3c003c00u, lg);
+          }
 #pragma unroll
           for (int w = 0; w < VEC / 2; ++w) {
             acc[g][2 * w] = dot2<kF16>(vlo[u][w], pp, acc[g][2 * w]);
@@ -556,7 +587,7 @@ void decode_kernel(const DecodeParams p) {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
           const float pi = pw[i][g];
-          lg += pi;
+          if constexpr (!PBC) lg += pi;
 #pragma unroll
           for (int e = 0; e < VEC; ++e) acc[g][e] = fmaf(pi, vf[i][e], acc[g][e]);
         }
@@ -621,11 +652,15 @@ void decode_kernel(const DecodeParams p) {
   // Rebase each stream from its lazy reference point onto its true maximum
   // (the partials carry the maximum, kernels/paged_attn_v3.cu:113-122).
   if constexpr (LAZY) {
-    if constexpr (PBC) {  // the heads' maxima live in the quad's lanes
+    if constexpr (PBC) {  // the heads' maxima and row sums live in the quad's lanes
       mx[0] = dpp_quad<0x00>(mx_own);
       mx[1] = dpp_quad<0x55>(mx_own);
       mx[2] = dpp_quad<0xAA>(mx_own);
       mx[3] = dpp_quad<0xFF>(mx_own);
+      l[0] = dpp_quad<0x00>(l_own);
+      l[1] = dpp_quad<0x55>(l_own);
+      l[2] = dpp_quad<0xAA>(l_own);
+      l[3] = dpp_quad<0xFF>(l_own);
     }
 #pragma unroll
     for (int g = 0; g < GC; ++g) {

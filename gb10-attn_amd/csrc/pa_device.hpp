@@ -316,6 +316,14 @@ __device__ inline float dpp(float v) {
 #define PA_DPP_MOV 1
 #endif
 template <int CTRL>
+__device__ inline uint32_t dpp_quad_u(uint32_t v) {
+  static_assert(CTRL >= 0 && CTRL <= 0xff, "quad permutations only");
+  if constexpr (PA_DPP_MOV)
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, false);
+  else
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
 __device__ inline float dpp_quad(float v) {
   static_assert(CTRL >= 0 && CTRL <= 0xff, "quad permutations only");
   if constexpr (PA_DPP_MOV)
