@@ -65,6 +65,12 @@
 #ifndef PA_DECODE_COMPACT
 #define PA_DECODE_COMPACT 1  // ragged batches: the work-groups a sequence needs first, the idle ones last
 #endif
+#ifndef PA_DECODE_F8PERM
+#define PA_DECODE_F8PERM 1  // FP8 P.V pairs: interleave two tokens' codes, then convert (no pair shuffles)
+#endif
+#ifndef PA_DECODE_SADDR
+#define PA_DECODE_SADDR 1  // GQA groups: scalar-base loads and a 32-bit block-id check
+#endif
 #ifndef PA_DECODE_MFMA
 #define PA_DECODE_MFMA 1  // GQA groups of >= 4 heads on the matrix-core kernel
 #endif
@@ -310,6 +316,12 @@ void decode_kernel(const DecodeParams p) {
   const uint32_t lane_off = (uint32_t)(sub * VEC * KV::kBytes);
   const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
   const uint64_t nb = (uint64_t)p.num_blocks;
+  // The same range check in 32 bits (a scalar compare for a wave-uniform
+  // block id instead of a 64-bit vector one): block ids are int32, so a pool
+  // of more than 2^31 blocks accepts every non-negative one, and a negative
+  // id reads as >= 2^31.
+  const uint32_t nb32 = nb > 0x80000000ull ? 0x80000000u : (uint32_t)nb;
+  constexpr bool SADDR = PA_DECODE_SADDR && GC > 1;
 
   // One wave tile in flight: raw K/V rows of NI tokens per lane and which of
   // them are live (inside the partition, on a page with a valid block id).
@@ -360,6 +372,15 @@ void decode_kernel(const DecodeParams p) {
   const uint32_t lane_row_k = (uint32_t)slot * k_st + lane_off;
   const uint32_t lane_row_v = (uint32_t)slot * v_st + lane_off;
   auto issue_fast = [&](int tile, int cp, int ct1, Tile& T) {
+    // GQA groups (bound by vector issue): the lanes' row offsets re-enter
+    // the block through an empty asm, so the 32 -> 64-bit extension of the
+    // address sits next to the loads and they take the scalar-base form
+    // (SGPR base + 32-bit VGPR offset) instead of a 64-bit VGPR address
+    // built by three vector instructions per load (FP8 config 3 +2.7 %;
+    // one-head work-groups, bound by HBM, measured -0.2 to -1 % and keep
+    // the plain form).
+    uint32_t ork = lane_row_k, orv = lane_row_v;
+    if constexpr (SADDR) asm volatile("" : "+v"(ork), "+v"(orv));
     int off0[NI], braw[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {  // all block-id reads first: one LDS round trip per tile
@@ -374,13 +395,13 @@ void decode_kernel(const DecodeParams p) {
       const int ti = tile + i * TPI;
       const int blk = __builtin_amdgcn_readfirstlane(braw[i]);
       const bool inrange = ti < ct1;
-      const bool okb = inrange && (uint64_t)(int64_t)blk < nb;
+      const bool okb = inrange && (SADDR ? (uint32_t)blk < nb32 : (uint64_t)(int64_t)blk < nb);
       bad |= (inrange && !okb) ? 1 : 0;
       const uint32_t use = okb ? 1u : 0u;
       const uint64_t rk = (uint64_t)((uint32_t)blk * use) * k_sb + (uint32_t)off0[i] * use * k_st;
       const uint64_t rv = (uint64_t)((uint32_t)blk * use) * v_sb + (uint32_t)off0[i] * use * v_st;
-      T.k[i] = load_raw<KV, PA_DECODE_NT>(kbase + rk, lane_row_k);
-      T.v[i] = load_raw<KV, PA_DECODE_NT>(vbase + rv, lane_row_v);
+      T.k[i] = load_raw<KV, PA_DECODE_NT>(kbase + rk, ork);
+      T.v[i] = load_raw<KV, PA_DECODE_NT>(vbase + rv, orv);
       live |= (okb && ti + slot < ct1) ? (1u << i) : 0u;
     }
     T.live = live;
@@ -460,7 +481,22 @@ void decode_kernel(const DecodeParams p) {
     // two tokens (vlo: element 2w of tokens 2u and 2u+1, vhi: element 2w+1).
     float vf[PVP ? 1 : NI][PVP ? 1 : VEC];
     uint32_t vlo[PVP ? NI / 2 : 1][PVP ? VEC / 2 : 1], vhi[PVP ? NI / 2 : 1][PVP ? VEC / 2 : 1];
-    if constexpr (PVP) {
+    if constexpr (PVP && KV::kCode == kFP8 && PA_DECODE_F8PERM) {
+      // FP8: interleave the two tokens' codes byte by byte first (two
+      // v_perm_b32 per code word of each token), so that each packed
+      // conversion yields a cross-token fp16 pair directly.
+#pragma unroll
+      for (int u = 0; u < NI / 2; ++u)
+#pragma unroll
+        for (int j = 0; j < VEC / 4; ++j) {
+          const uint32_t x0 = __builtin_amdgcn_perm(vr[2 * u + 1][j], vr[2 * u][j], 0x05010400u);
+          const uint32_t x1 = __builtin_amdgcn_perm(vr[2 * u + 1][j], vr[2 * u][j], 0x07030602u);
+          vlo[u][2 * j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x0, 1.0f, false));
+          vhi[u][2 * j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x0, 1.0f, true));
+          vlo[u][2 * j + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x1, 1.0f, false));
+          vhi[u][2 * j + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x1, 1.0f, true));
+        }
+    } else if constexpr (PVP) {
       uint32_t vp[NI][VEC / 2];
 #pragma unroll
       for (int i = 0; i < NI; ++i) KV::template to_pairs<kF16>(vr[i], vp[i]);
