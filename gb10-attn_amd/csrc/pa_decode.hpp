@@ -69,7 +69,7 @@
 #define PA_DECODE_F8PERM 1  // FP8 P.V pairs: interleave two tokens' codes, then convert (no pair shuffles)
 #endif
 #ifndef PA_DECODE_SADDR
-#define PA_DECODE_SADDR 1  // GQA groups: scalar-base loads and a 32-bit block-id check
+#define PA_DECODE_SADDR 1  // GQA groups and FP8 caches: scalar-base loads and a 32-bit block-id check
 #endif
 #ifndef PA_DECODE_MFMA
 #define PA_DECODE_MFMA 1  // GQA groups of >= 4 heads on the matrix-core kernel
@@ -321,7 +321,7 @@ void decode_kernel(const DecodeParams p) {
   // of more than 2^31 blocks accepts every non-negative one, and a negative
   // id reads as >= 2^31.
   const uint32_t nb32 = nb > 0x80000000ull ? 0x80000000u : (uint32_t)nb;
-  constexpr bool SADDR = PA_DECODE_SADDR && GC > 1;
+  constexpr bool SADDR = PA_DECODE_SADDR && (GC > 1 || KV::kCode == kFP8);
 
   // One wave tile in flight: raw K/V rows of NI tokens per lane and which of
   // them are live (inside the partition, on a page with a valid block id).
@@ -372,13 +372,13 @@ void decode_kernel(const DecodeParams p) {
   const uint32_t lane_row_k = (uint32_t)slot * k_st + lane_off;
   const uint32_t lane_row_v = (uint32_t)slot * v_st + lane_off;
   auto issue_fast = [&](int tile, int cp, int ct1, Tile& T) {
-    // GQA groups (bound by vector issue): the lanes' row offsets re-enter
-    // the block through an empty asm, so the 32 -> 64-bit extension of the
-    // address sits next to the loads and they take the scalar-base form
-    // (SGPR base + 32-bit VGPR offset) instead of a 64-bit VGPR address
-    // built by three vector instructions per load (FP8 config 3 +2.7 %;
-    // one-head work-groups, bound by HBM, measured -0.2 to -1 % and keep
-    // the plain form).
+    // GQA groups and FP8 caches (bound by vector issue): the lanes' row
+    // offsets re-enter the block through an empty asm, so the 32 -> 64-bit
+    // extension of the address sits next to the loads and they take the
+    // scalar-base form (SGPR base + 32-bit VGPR offset) instead of a 64-bit
+    // VGPR address built by three vector instructions per load (FP8 config
+    // 3 +2.7 %, FP8 config 2 +1 %; 16-bit MHA work-groups, bound by HBM,
+    // measured -0.2 to -1 % and keep the plain form).
     uint32_t ork = lane_row_k, orv = lane_row_v;
     if constexpr (SADDR) asm volatile("" : "+v"(ork), "+v"(orv));
     int off0[NI], braw[NI];
