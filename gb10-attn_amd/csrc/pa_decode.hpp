@@ -65,6 +65,9 @@
 #ifndef PA_DECODE_COMPACT
 #define PA_DECODE_COMPACT 1  // ragged batches: the work-groups a sequence needs first, the idle ones last
 #endif
+#ifndef PA_DECODE_BTPF
+#define PA_DECODE_BTPF 1  // fetch the first block-table chunk with the context length
+#endif
 #ifndef PA_DECODE_F8PERM
 #define PA_DECODE_F8PERM 1  // FP8 P.V pairs: interleave two tokens' codes, then convert (no pair shuffles)
 #endif
@@ -229,6 +232,19 @@ void decode_kernel(const DecodeParams p) {
     if (!(qa >= 0 && qe == qa + 1 && (int64_t)qe <= p.q_total)) return;  // work-group uniform
     zq = qa;
   }
+
+  // The first block-table chunk of the partition is fetched before the
+  // context length has arrived when its first page is known without it (the
+  // first partition, or fixed-length partitions): the K/V loads then wait for
+  // one memory round trip less at start-up (config 2 +0.2 %, FP8 config 3
+  // +0.7 %).  Packed 16-bit MHA rows (config 5) measured -2.5 % with it and
+  // keep the plain order.
+  constexpr bool BTPF = PA_DECODE_BTPF && !(GC == 1 && HP > 1 && KV::kCode != kFP8);
+  const bool bt_early = BTPF && (p.part_tokens > 0 || part == 0);
+  const int pg_early = p.part_tokens > 0 ? (int)(((int64_t)part * p.part_tokens) / p.BS) : 0;
+  int32_t bt_pre = 0;
+  if (bt_early && pg_early + (int)threadIdx.x < p.MB)
+    bt_pre = p.block_tables[(int64_t)b * p.bt_stride + pg_early + threadIdx.x];
 
   const int maxctx = p.MB * p.BS;
   const int ctx_b = p.context_lens[b];
@@ -639,7 +655,12 @@ void decode_kernel(const DecodeParams p) {
     for (int cp = pg0; cp < pg1; cp += kBtChunk) {
       const int np = min(kBtChunk, pg1 - cp);
       __syncthreads();
-      for (int i = threadIdx.x; i < np; i += kDecodeThreads) s_bt[i] = bt_row[cp + i];
+      if (bt_early && cp == pg0) {
+        static_assert(kBtChunk <= kDecodeThreads, "one prefetched entry per thread");
+        if ((int)threadIdx.x < np) s_bt[threadIdx.x] = bt_pre;
+      } else {
+        for (int i = threadIdx.x; i < np; i += kDecodeThreads) s_bt[i] = bt_row[cp + i];
+      }
       __syncthreads();
       const int ct0 = max(t0, cp * p.BS);
       const int ct1 = min(t1, (cp + np) * p.BS);
