@@ -671,3 +671,23 @@ def test_fp8_gqa4_two_kv_heads_per_work_group(pa, dev, D, qt):
             assert f"{D}, 4, 2, " in pa.last_launch(), pa.last_launch()
         assert np.isfinite(got).all(), ns
         close(got, want)
+
+
+@pytest.mark.parametrize("kv,H,HKV,qt", [("f16", 4, 4, "f32"), ("bf16", 8, 2, "bf16"), ("f16", 8, 2, "f16")])
+def test_compacted_grid_ragged_split(pa, dev, kv, H, HKV, qt):
+    """The automatic v3 plan with fixed-length partitions over a ragged batch
+    of at most 64 sequences, whose grid is numbered compactly (each sequence's
+    needed partitions first, the idle work-groups last): an empty row, a row
+    longer than the table, a one-token row, rows of one, several and all
+    partitions in one launch, each against the oracle."""
+    ctxs = [0, 48, 1, 300, 4096, 2049, 17]
+    inp = decode_case(len(ctxs), H, HKV, 64, 16, ctxs, seed=31, kv=kv, q=qt, mb=256)
+    q, k, v, bt, _ = dev_inputs(inp, dev)
+    ctx = inp["ctx"].copy()
+    ctx[1] = 256 * 16 + 1  # beyond MB*BS: NaN row, no read past the table
+    assert pa.workspace_size(q, k, bt, 0) > 0, "the plan must split for this case"
+    got = to_host(run(pa, "v3auto", q, k, v, bt, torch.from_numpy(ctx).to(dev), 0.125, out_dtype=torch.float32))
+    assert np.all(got[0] == 0.0)
+    assert np.all(np.isnan(got[1]))
+    want = oracle.decode(inp["q_f32"], inp["k"], inp["v"], inp["bt"], ctx, 0.125, kv)
+    close(got[2:], want[2:])
