@@ -97,7 +97,10 @@ constexpr float kDmLazy = 8.0f;  // raise the running max only past 2^8
 #define PA_DM_KNT 0
 #endif
 
-template <typename KV, int D, int GC>
+// SQ: q may need the hi + lo split (q's dtype is not the cache's).  A
+// separate instance for q of the cache's dtype keeps the run-time test out of
+// the k-step loop, where it put a branch between consecutive MFMAs.
+template <typename KV, int D, int GC, bool SQ>
 __global__ __launch_bounds__(256) void decode_mfma_kernel(const DecodeParams p) {
   using Sh = DmShape<D>;
   constexpr int KT = Sh::KT, KS = Sh::KS, NDT = Sh::NDT, NCH = Sh::NCH, TPD = Sh::TPD, NDMA = Sh::NDMA;
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(const DecodeParams p) 
   // Q^T operand: head column col (zero past the group), dims 32*ks + kg*8 .. +8,
   // in the KV type (hi + lo when q is another type).
   const bool qlive = col < GC && g0 + col < p.G;
-  const bool split_q = p.q_dtype != KV::kCode;
+  const bool split_q = SQ && p.q_dtype != KV::kCode;
   u32x4_t qf[KS], qlo[KS];
   {
     const int64_t qb = ((int64_t)z * p.H + kvh * p.G + g0 + (qlive ? col : 0)) * D + kg * 8;
@@ -430,7 +433,10 @@ template <typename KV, int D, int GC>
 hipError_t launch_decode_mfma_dg(const DecodeParams& p, hipStream_t stream) {
   const int64_t blocks = (int64_t)p.B * p.Sq * p.HKV * p.head_chunks * p.parts;
   note_launch("pa::decode_mfma_kernel<%s, %d, %d>", KV::kName, D, GC);
-  hipLaunchKernelGGL((decode_mfma_kernel<KV, D, GC>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+  if (p.q_dtype == KV::kCode)
+    hipLaunchKernelGGL((decode_mfma_kernel<KV, D, GC, false>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((decode_mfma_kernel<KV, D, GC, true>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
