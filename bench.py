@@ -257,17 +257,22 @@ def _gather_pages(k, v, bt, ctx, BS, scale=None):
     return kh.cpu().numpy(), vh.cpu().numpy(), np.ascontiguousarray(remap[bt].astype(np.int32))
 
 
-def check_decode(work, nseq=2):
-    """One v3 call on pool 0 (the plan the timed loop runs); the sampled
-    sequences (the longest and shortest, else the first and last) against the
-    oracle's cpu_reference restatement.  Also returns the dispatched kernels."""
+def check_decode(work, nseq=2, entry="v3"):
+    """One call on pool 0 (v3: the plan the timed loop runs; v1 / v2: the
+    reference's other decode entry points); the sampled sequences (the longest
+    and shortest, else the first and last) against the oracle's cpu_reference
+    restatement.  Also returns the dispatched kernels."""
     import oracle
     ctx = work.ctx_host
     seqs = sorted({int(np.argmax(ctx)), int(np.argmin(ctx))} if ctx.min() != ctx.max() else {0, work.B - 1})[:nseq]
     work.out.fill_(float("nan"))
     a = work.args[0]
-    rc = work.L.paged_attention_v3_scaled(*a, work.scale, work.kv_scale or 1.0, work.kv_scale or 1.0, work.num_splits,
-                                          work.ws.data_ptr(), work.ws_bytes, torch.cuda.current_stream().cuda_stream)
+    sp = torch.cuda.current_stream().cuda_stream
+    if entry == "v3":
+        rc = work.L.paged_attention_v3_scaled(*a, work.scale, work.kv_scale or 1.0, work.kv_scale or 1.0,
+                                              work.num_splits, work.ws.data_ptr(), work.ws_bytes, sp)
+    else:
+        rc = getattr(work.L, "paged_attention" if entry == "v1" else "paged_attention_v2")(*a, work.scale, sp)
     if rc != 0:
         raise RuntimeError(work.pa.last_error())
     kernels = work.pa.last_launch()
@@ -862,12 +867,14 @@ def decode_record(work, steps, warmup):
 # The reference's v3 per-call times at the sweep's points, NVIDIA GB10
 # (results/c000-20260901-225701-verify/{cold,hot}_b{B}_c{ctx}.txt:19; the
 # "hot" points' working sets already exceed GB10's 24 MiB L2; b64_c2048 from
-# docs/REPORT.md:124, 402.65 MB / 231.3 GB/s).
+# docs/REPORT.md:124, 402.65 MB / 231.3 GB/s; b64_c4096 from docs/REPORT.md:125,
+# 805.3 MB / 227.6 GB/s).
 SWEEP_REF_US = {(1, 512): (21.7, "cold_b1_c512.txt:19"), (1, 2048): (34.4, "cold_b1_c2048.txt:19"),
                 (4, 512): (30.5, "cold_b4_c512.txt:19"), (4, 2048): (120.5, "cold_b4_c2048.txt:19"),
                 (16, 512): (116.7, "cold_b16_c512.txt:19"), (16, 2048): (464.2, "hot_b16_c2048.txt:19"),
                 (64, 512): (471.5, "hot_b64_c512.txt:19"), (64, 2048): (1740.8, "docs/REPORT.md:124"),
-                (128, 512): (907.8, "hot_b128_c512.txt:19")}
+                (128, 512): (907.8, "hot_b128_c512.txt:19"),
+                (64, 4096): (3538.2, "docs/REPORT.md:125")}
 
 
 def graph_us_per_call(work, calls):
@@ -897,8 +904,103 @@ def graph_us_per_call(work, calls):
     return t0.elapsed_time(t1) * 1e3 / (reps * calls)
 
 
+def _time_calls(fn, steps, warmup=5):
+    """Median over REPEATS of the mean time (ms) of `steps` back-to-back fn(i)
+    (i indexes the rotating block-table sets), HIP events on the launch stream."""
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    reps, n = [], warmup
+    for _ in range(REPEATS):
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for i in range(steps):
+            fn(n + i)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        reps.append(t0.elapsed_time(t1) / steps)
+        n += steps
+    return float(np.median(reps))
+
+
+def sweep_legs(w, steps):
+    """The paths the reference prints beside v3 at each sweep point
+    (results/c000-20260901-225701-verify/cold_b16_c512.txt:15-19), timed on
+    the same rotating block-table sets, each behind its correctness check:
+    v1 and v2 (paged_attention, paged_attention_v2: one partition per
+    (sequence, head unit)), and on the GPU through torch the pages gathered
+    into a dense [B, H, ctx, D] layout then attended densely (fp32 scores,
+    softmax, weighted sum) or by torch's fused SDPA (flash / memory-efficient
+    backends only; fp16 operands made contiguous)."""
+    import oracle
+    legs = {}
+    sp = torch.cuda.current_stream().cuda_stream
+    for name, entry in (("v1", "paged_attention"), ("v2", "paged_attention_v2")):
+        chk, kern = check_decode(w, entry=name)
+        leg = {"check_ok": chk["ok"], "max_abs": chk["max_abs"], "kernels": kern}
+        if chk["ok"]:
+            f = getattr(w.L, entry)
+
+            def call(i, f=f):
+                if f(*w.args[i % w.pools], w.scale, sp) != 0:
+                    raise RuntimeError(w.pa.last_error())
+            us = _time_calls(call, steps) * 1e3
+            leg.update(us_per_call=round(us, 2), GBs=round(w.bytes / (us * 1e-6) / 1e9, 1))
+        legs[name] = leg
+    B, H, D, BS = w.B, w.H, w.D, w.BS
+    ctx = int(w.ctx_host[0])
+    pages = -(-ctx // BS)
+    q16 = w.q.view(B, H, 1, D)
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    def gathered(i):
+        idx = w.bt[i % w.pools][:, :pages].reshape(-1).long()
+        kg = w.k[0].index_select(0, idx).view(B, pages * BS, H, D)[:, :ctx]
+        vg = w.v[0].index_select(0, idx).view(B, pages * BS, H, D)[:, :ctx]
+        return kg, vg
+
+    def dense(i):
+        kg, vg = gathered(i)
+        kt = kg.permute(0, 2, 3, 1).float().contiguous()  # [B, H, D, ctx]
+        vt = vg.permute(0, 2, 1, 3).float().contiguous()  # [B, H, ctx, D]
+        p = torch.softmax(torch.matmul(q16.float(), kt) * w.scale, dim=-1)
+        return torch.matmul(p, vt).view(B, H, D)
+
+    def sdpa(i):
+        kg, vg = gathered(i)
+        kt = kg.permute(0, 2, 1, 3).contiguous()
+        vt = vg.permute(0, 2, 1, 3).contiguous()
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            return torch.nn.functional.scaled_dot_product_attention(q16, kt, vt, scale=w.scale).view(B, H, D)
+
+    ctxh = w.ctx_host
+    seqs = sorted({0, B - 1})
+    k, v, bts = _gather_pages(w.k[0], w.v[0], w.bt_host[seqs], ctxh[seqs], BS)
+    want = oracle.decode(w.q[seqs].float().cpu().numpy(), k, v, bts, ctxh[seqs], w.scale, "f32")
+    for name, fn in (("gather_dense_torch", dense), ("gather_sdpa_torch", sdpa)):
+        try:
+            got = fn(0)
+        except RuntimeError as e:  # no fused SDPA backend for this shape / device
+            legs[name] = {"unavailable": str(e).splitlines()[0][:160]}
+            continue
+        torch.cuda.synchronize()
+        chk = _compare(got[seqs].float().cpu().numpy(), want, f"sequences {seqs} vs oracle.decode")
+        leg = {"check_ok": chk["ok"], "max_abs": chk["max_abs"]}
+        if chk["ok"]:
+            us = _time_calls(fn, max(5, steps // 4), 2) * 1e3
+            leg.update(us_per_call=round(us, 2), GBs=round(w.bytes / (us * 1e-6) / 1e9, 1))
+        legs[name] = leg
+    return legs
+
+
+SWEEP_POINTS = [(B, c) for B in (1, 4, 16, 64, 128) for c in (512, 2048)] + [(64, 4096)]
+
+
 def sweep_records(pa, steps):
-    """The reference's small-batch cold sweep, B in {1,4,16,64,128} x ctx in {512,2048}."""
+    """The reference's small-batch cold sweep, B in {1,4,16,64,128} x ctx in
+    {512,2048}, and its 805 MB point B=64 ctx=4096 (docs/REPORT.md:125); v3
+    timed as whole calls and in a graph, v1 / v2 / torch paths beside it."""
     dev = torch.device("cuda:0")
     BS, H, D = 16, 12, 64
     blk_bytes = BS * H * D * 2
@@ -908,34 +1010,35 @@ def sweep_records(pa, steps):
     k = torch.randn((nb, BS, H, D), generator=g, device=dev, dtype=torch.float32).half()
     v = torch.randn((nb, BS, H, D), generator=g, device=dev, dtype=torch.float32).half()
     out = []
-    for B in (1, 4, 16, 64, 128):
-        for ctx in (512, 2048):
-            w = SweepWorkload(pa, (k, v), B=B, ctx=ctx, seed=B * 10000 + ctx)
-            log(f"bench: sweep B={B} ctx={ctx} ({w._sets} block-table sets, {w.footprint_gb():.2f} GB)")
-            chk, kernels = check_decode(w)
-            if not chk["ok"]:
-                out.append(failed_record(w.name, chk, kernels))
-                continue
-            w.split = False  # time whole calls (partition + reduce)
-            ms, _, _ = timed(w, max(steps, 50), 10)
-            # The graph's calls cover >= 1.1 GB of distinct pages, so its replays stay cold too.
-            gus = graph_us_per_call(w, min(w._sets, max(4, -(-int(1.1e9) // int(w.bytes))), 1024))
-            ref_us, ref_src = SWEEP_REF_US.get((B, ctx), (None, None))
-            us = ms * 1e3
-            rec = {"workload": w.name, "batch": B, "context_len": ctx, "us_per_call": round(us, 2),
-                   "GBs": round(w.bytes / (us * 1e-6) / 1e9, 1),
-                   "frac_of_8TBs": round(w.bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
-                   "us_per_call_graph": round(gus, 2),
-                   "GBs_graph": round(w.bytes / (gus * 1e-6) / 1e9, 1),
-                   "frac_of_8TBs_graph": round(w.bytes / (gus * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
-                   "bytes_per_call": int(w.bytes), "split": w.ws_bytes > 0, "kernels": kernels,
-                   "block_table_sets": w._sets, "footprint_GB": round(w.footprint_gb(), 2), "check": chk}
-            if ref_us:
-                rec["reference_gb10_us"] = ref_us
-                rec["reference_source"] = "results/c000-20260901-225701-verify/" + ref_src \
-                    if ref_src.endswith(":19") else ref_src
-            out.append(rec)
-            del w
+    for B, ctx in SWEEP_POINTS:
+        w = SweepWorkload(pa, (k, v), B=B, ctx=ctx, seed=B * 10000 + ctx)
+        log(f"bench: sweep B={B} ctx={ctx} ({w._sets} block-table sets, {w.footprint_gb():.2f} GB)")
+        chk, kernels = check_decode(w)
+        if not chk["ok"]:
+            out.append(failed_record(w.name, chk, kernels))
+            continue
+        w.split = False  # time whole calls (partition + reduce)
+        ms, _, _ = timed(w, max(steps, 50), 10)
+        # The graph's calls cover >= 1.1 GB of distinct pages, so its replays stay cold too.
+        gus = graph_us_per_call(w, min(w._sets, max(4, -(-int(1.1e9) // int(w.bytes))), 1024))
+        ref_us, ref_src = SWEEP_REF_US.get((B, ctx), (None, None))
+        us = ms * 1e3
+        rec = {"workload": w.name, "batch": B, "context_len": ctx, "us_per_call": round(us, 2),
+               "GBs": round(w.bytes / (us * 1e-6) / 1e9, 1),
+               "frac_of_8TBs": round(w.bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+               "us_per_call_graph": round(gus, 2),
+               "GBs_graph": round(w.bytes / (gus * 1e-6) / 1e9, 1),
+               "frac_of_8TBs_graph": round(w.bytes / (gus * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+               "bytes_per_call": int(w.bytes), "split": w.ws_bytes > 0, "kernels": kernels,
+               "block_table_sets": w._sets, "footprint_GB": round(w.footprint_gb(), 2), "check": chk}
+        if ref_us:
+            rec["reference_gb10_us"] = ref_us
+            rec["reference_source"] = "results/c000-20260901-225701-verify/" + ref_src \
+                if ref_src.endswith(":19") else ref_src
+        log(f"bench: sweep B={B} ctx={ctx}: v1, v2, torch gather paths")
+        rec["beside_v3"] = sweep_legs(w, max(20, steps // 2))
+        out.append(rec)
+        del w
     return out
 
 
@@ -1009,6 +1112,29 @@ def prefill_record(work, steps, warmup):
         "dtype": str(work.dtype).replace("torch.", ""),
         "kv_dtype": str(work.k.dtype).replace("torch.", ""), "kernels": kernels, "check": chk,
     }
+
+
+def summarize(line):
+    """Every workload of the line in a few numbers: [value, unit, fraction of
+    its roofline, ms per step] (decode: of 8 TB/s; prefill: of the 2.5 PFLOP/s
+    dense peak); sweep points add the v1 / v2 / torch gather-dense / torch
+    SDPA GB/s measured beside v3 (null when unavailable or failed)."""
+    out = {line["config"]["workload"]: [line["value"], line["unit"], line["roofline"]["frac"], line["ms_per_step"]]}
+    for r in line.get("also", []):
+        name = r.get("workload")
+        if not name or r.get("status") == "FAILED":
+            if name:
+                out[name] = "FAILED"
+            continue
+        if name.startswith("sweep_"):
+            legs = r.get("beside_v3", {})
+            out[name] = [r["GBs"], "GB/s", r["frac_of_8TBs"], round(r["us_per_call"] / 1e3, 5),
+                         {k: legs.get(k, {}).get("GBs") for k in ("v1", "v2", "gather_dense_torch",
+                                                                  "gather_sdpa_torch")}]
+        elif "value" in r and "unit" in r:
+            frac = r.get("frac_of_8TBs", r.get("frac_of_mfma_peak"))
+            out[name] = [r["value"], r["unit"], frac, r.get("ms_per_step")]
+    return out
 
 
 def main():
@@ -1162,6 +1288,7 @@ def main():
         log("bench: per-call host overhead")
         also.append(call_overhead(pa))
     line["also"] = also
+    line["summary"] = summarize(line)  # last key: survives a truncated tail of this line
     print(json.dumps(line), flush=True)
 
 

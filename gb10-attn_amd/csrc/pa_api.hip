@@ -162,40 +162,19 @@ int scratch_address(void** ptr) {
   return PA_OK;
 }
 
-// Tuning constants of the partition planner (compile-time; a sweep build
-// overrides them with -D): target resident work-groups per CU; the shortest
-// partition worth a work-group (and the same for tiny grids, whose time is
-// latency, not bandwidth) and the longest (bounds ragged imbalance), in
-// tokens; the longest when the plan splits anyway and the VALU kernel serves
-// the group (finer balance for ragged batches, config 3: +4 %; the
-// matrix-core kernel, groups of 8+, amortises its set-up over the longer
-// one); and a fixed head packing (> 0: KV heads per work-group for packable
-// layouts, whatever the split; 0: the planner's choice).
-#ifndef PA_PLAN_WGS_PER_CU
-#define PA_PLAN_WGS_PER_CU 3
-#endif
-#ifndef PA_PLAN_MIN_PART
-#define PA_PLAN_MIN_PART 256
-#endif
-#ifndef PA_PLAN_MIN_PART_TINY
-#define PA_PLAN_MIN_PART_TINY 64
-#endif
-#ifndef PA_PLAN_MAX_PART
-#define PA_PLAN_MAX_PART 2048
-#endif
-#ifndef PA_PLAN_MAX_PART_SPLIT
-#define PA_PLAN_MAX_PART_SPLIT 1024
-#endif
-#ifndef PA_PLAN_PACK
-#define PA_PLAN_PACK 0
-#endif
+// Tuning constants of the partition planner: target resident work-groups
+// per CU; the shortest partition worth a work-group (and the same for tiny
+// grids, whose time is latency, not bandwidth) and the longest (bounds ragged
+// imbalance), in tokens; the longest when the plan splits anyway and the VALU
+// kernel serves the group (finer balance for ragged batches, config 3: +4 %;
+// the matrix-core kernel, groups of 8+, amortises its set-up over the longer
+// one).
 struct PlanKnobs {
-  int64_t wgs_per_cu = PA_PLAN_WGS_PER_CU;
-  int64_t min_part = PA_PLAN_MIN_PART;
-  int64_t min_part_tiny = PA_PLAN_MIN_PART_TINY;
-  int64_t max_part = PA_PLAN_MAX_PART;
-  int64_t max_part_split = PA_PLAN_MAX_PART_SPLIT;
-  int64_t pack = PA_PLAN_PACK;
+  int64_t wgs_per_cu = 3;
+  int64_t min_part = 256;
+  int64_t min_part_tiny = 64;
+  int64_t max_part = 2048;
+  int64_t max_part_split = 1024;
 };
 
 const PlanKnobs& knobs() {
@@ -210,6 +189,11 @@ struct DecodeArgs {
   int kv_dtype;
   int gc;
 };
+
+// The kernels take scales as fp32: a finite double past FLT_MAX would become
+// inf there, so every scale (and the folded softmax scale) is checked as fp32.
+static bool finite_f32(double x) { return std::isfinite((float)x); }
+
 
 // Shared checks of every entry point (the TORCH_CHECKs of
 // kernels/paged_attn_v3.cu:199-216 and kernels/paged_attn_prefill.cu:128-146,
@@ -244,7 +228,8 @@ int check_args(const pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* 
   if (!is_contiguous(out)) return fail(PA_ERR_INVALID_ARGUMENT, "out must be contiguous");
   for (int i = 0; i < 4; ++i)
     if (v->shape[i] != k->shape[i]) return fail(PA_ERR_INVALID_ARGUMENT, "v_cache must have the shape of k_cache");
-  if (!std::isfinite(scale)) return fail(PA_ERR_INVALID_ARGUMENT, "scale must be finite");
+  if (!std::isfinite(scale) || !finite_f32(scale * 1.4426950408889634))
+    return fail(PA_ERR_INVALID_ARGUMENT, "scale must be finite");
 
   const int64_t B = q->shape[0];
   const int64_t S = prefill ? q->shape[1] : 1;
@@ -358,16 +343,6 @@ int make_plan(const DecodeParams& p, int gc, int kv_bytes, int64_t num_splits, P
     return np;
   };
   int64_t ptok = 0;
-  if (knobs().pack > 0) {  // fixed packing (measurement knob)
-    int c = hi;
-    while (c > lo && c > knobs().pack) c /= 2;
-    const int64_t np = parts_for(c, &ptok);
-    plan->parts = np;
-    plan->part_tokens = np > 1 ? ptok : 0;
-    plan->direct = np <= 1;
-    plan->hp = c;
-    return PA_OK;
-  }
   const int64_t nparts = parts_for(lo, &ptok);
   int hp = lo;
   // A grid that does not fill the GPU even unpacked keeps every work-group
@@ -439,8 +414,10 @@ int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const p
   int rc = check_args(out, q, k, v, bt, ctx, scale, false, &a);
   if (rc) return rc;
   if (noalloc) ws_bytes = PA_NOALLOC_SCRATCH_BYTES;  // the split scratch is this device's fixed array
-  if (!std::isfinite(k_scale) || !std::isfinite(v_scale))
+  if (!finite_f32(k_scale) || !finite_f32(v_scale))
     return fail(PA_ERR_INVALID_ARGUMENT, "k_scale and v_scale must be finite");
+  if (!finite_f32(scale * k_scale * 1.4426950408889634))
+    return fail(PA_ERR_INVALID_ARGUMENT, "scale * k_scale must be finite");
   // Dequantisation scales of the cache (FP8): k_scale joins the softmax
   // scale, v_scale multiplies the weighted V sum.
   a.p.qscale = (float)(scale * k_scale * 1.4426950408889634);
@@ -694,7 +671,7 @@ int paged_attention_prefill_wmma_scaled(pa_tensor_t* out, const pa_tensor_t* q, 
                                         const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
                                         const pa_tensor_t* context_lens, double scale, double k_scale,
                                         double v_scale, void* stream) {
-  if (!std::isfinite(k_scale) || !std::isfinite(v_scale))
+  if (!finite_f32(k_scale) || !finite_f32(v_scale))
     return fail(PA_ERR_INVALID_ARGUMENT, "k_scale and v_scale must be finite");
   // k_scale joins the softmax scale (q . (k_scale k) = (scale k_scale) q . k),
   // v_scale multiplies the output rows.
@@ -718,7 +695,7 @@ int paged_attention_prefill_varlen_scaled(pa_tensor_t* out, const pa_tensor_t* q
                                           int64_t max_q_len, double scale, double k_scale, double v_scale,
                                           void* stream) {
   int rc;
-  if (!std::isfinite(k_scale) || !std::isfinite(v_scale))
+  if (!finite_f32(k_scale) || !finite_f32(v_scale))
     return fail(PA_ERR_INVALID_ARGUMENT, "k_scale and v_scale must be finite");
   if ((rc = check_tensor(q, "q", 3, "[T, H, D]"))) return rc;
   if ((rc = check_tensor(out, "out", 3, "[T, H, D]"))) return rc;
@@ -792,7 +769,7 @@ int pa_write_kv_scaled(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tens
   if (cd != kF16 && cd != kBF16 && cd != kF32 && cd != kFP8)
     return fail(PA_ERR_INVALID_ARGUMENT, "k_cache must be float16, bfloat16, float32 or float8_e4m3fn (got %s)",
                 dtype_name(cd));
-  if (!std::isfinite(k_scale) || !std::isfinite(v_scale) || (float)k_scale == 0.0f || (float)v_scale == 0.0f)
+  if (!finite_f32(k_scale) || !finite_f32(v_scale) || (float)k_scale == 0.0f || (float)v_scale == 0.0f)
     return fail(PA_ERR_INVALID_ARGUMENT, "k_scale and v_scale must be finite and nonzero");
   if (v_cache->dtype != cd) return fail(PA_ERR_INVALID_ARGUMENT, "v_cache must have the dtype of k_cache");
   if (sd != kF16 && sd != kBF16 && sd != kF32)

@@ -151,18 +151,9 @@ hipError_t launch_write_kv(const WriteParams& p, hipStream_t stream);
 // only K (the workspace-size query has no V), and the kernel also needs V's
 // heads contiguous, else it serves one head per work-group under the same
 // plan.
-#ifndef PA_PACK_ROW_BYTES
-#define PA_PACK_ROW_BYTES 512  // widest packed row
-#endif
-#ifndef PA_PACK_MAX
-#define PA_PACK_MAX 4  // most KV heads per work-group
-#endif
-#ifndef PA_PACK_GQA_MAX
-#define PA_PACK_GQA_MAX 2  // most KV heads per work-group for GQA groups of four
-#endif
-#ifndef PA_PACK_GQA_ROW_BYTES
-#define PA_PACK_GQA_ROW_BYTES 512  // widest packed row for GQA groups of four
-#endif
+constexpr int kPackRowBytes = 512;  // widest packed row
+constexpr int kPackMax = 4;         // most KV heads per work-group
+constexpr int kPackGqaMax = 2;      // most KV heads per work-group for GQA groups of four
 
 // Widest packing the layout allows (1 = none).  GQA groups of four query
 // heads over 8/16-bit caches pack too: each lane still serves one KV head's
@@ -171,8 +162,8 @@ hipError_t launch_write_kv(const WriteParams& p, hipStream_t stream);
 // 4550 -> 4753).
 inline int decode_pack_max(int D, int kv_bytes, int G, int HKV, int64_t k_sh) {
   if (k_sh != D || !(G == 1 || (G == 4 && kv_bytes <= 2))) return 1;
-  const int most = G == 1 ? PA_PACK_MAX : PA_PACK_GQA_MAX;
-  const int64_t row = G == 1 ? PA_PACK_ROW_BYTES : PA_PACK_GQA_ROW_BYTES;
+  const int most = G == 1 ? kPackMax : kPackGqaMax;
+  const int64_t row = kPackRowBytes;
   int hp = 1;
   for (int c = 2; c <= most; c *= 2)
     if ((int64_t)D * kv_bytes * c <= row && HKV % c == 0) hp = c;

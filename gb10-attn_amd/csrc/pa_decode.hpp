@@ -30,54 +30,6 @@
 
 #include <atomic>
 
-// Loop-structure knobs (compile-time): K/V loads per lane per tile, and
-// whether K/V loads carry the non-temporal (streaming) hint.
-#ifndef PA_DECODE_NI
-#define PA_DECODE_NI 4
-#endif
-#ifndef PA_DECODE_NI_MHA
-#define PA_DECODE_NI_MHA 2  // loads per lane per tile for one unpacked MHA head per work-group (config 2: +0.8 % over 4)
-#endif
-#ifndef PA_DECODE_NT
-#define PA_DECODE_NT 1
-#endif
-#ifndef PA_DECODE_WAVES
-#define PA_DECODE_WAVES 4
-#endif
-#ifndef PA_DECODE_LAZY
-#define PA_DECODE_LAZY 1  // raise the softmax reference point only by more than 2^8
-#endif
-#ifndef PA_DECODE_ROT
-#define PA_DECODE_ROT 1  // rotate the head order per (sequence, partition) for one-head work-groups
-#endif
-#ifndef PA_DECODE_PBCAST
-#define PA_DECODE_PBCAST 1  // groups of four heads: one exponential per lane, shared across the quad
-#endif
-#ifndef PA_DECODE_PVDOT
-#define PA_DECODE_PVDOT 1  // GQA groups over fp16/FP8 caches: P.V as packed fp16 dot products over token pairs
-#endif
-#ifndef PA_DECODE_DOT2
-#define PA_DECODE_DOT2 1  // packed dot products for q . k (16-bit caches, q of the cache's dtype)
-#endif
-#ifndef PA_DECODE_PPRIO
-#define PA_DECODE_PPRIO 1  // one-head work-groups of a fully resident grid: priority falls with progress
-#endif
-#ifndef PA_DECODE_COMPACT
-#define PA_DECODE_COMPACT 1  // ragged batches: the work-groups a sequence needs first, the idle ones last
-#endif
-#ifndef PA_DECODE_BTPF
-#define PA_DECODE_BTPF 1  // fetch the first block-table chunk with the context length
-#endif
-#ifndef PA_DECODE_F8PERM
-#define PA_DECODE_F8PERM 1  // FP8 P.V pairs: interleave two tokens' codes, then convert (no pair shuffles)
-#endif
-#ifndef PA_DECODE_SADDR
-#define PA_DECODE_SADDR 1  // GQA groups and FP8 caches: scalar-base loads and a 32-bit block-id check
-#endif
-#ifndef PA_DECODE_MFMA
-#define PA_DECODE_MFMA 1  // GQA groups of >= 4 heads on the matrix-core kernel
-#endif
-
 namespace pa {
 
 // Ragged batches with fixed-length partitions: the grid holds `parts`
@@ -91,7 +43,7 @@ namespace pa {
 // wave derives the numbering from the context lengths itself: one load per
 // lane and a prefix sum across the wave, hence at most 64 sequences.
 __device__ inline bool compact_grid(const DecodeParams& p) {
-  return PA_DECODE_COMPACT && p.part_tokens > 0 && p.Sq == 1 && p.B <= 64 && p.cu_q == nullptr;
+  return p.part_tokens > 0 && p.Sq == 1 && p.B <= 64 && p.cu_q == nullptr;
 }
 // Unit `id` of the compacted numbering -> (z, part); false past the last one.
 __device__ inline bool compact_unit(const DecodeParams& p, int id, int lane, int& z, int& part) {
@@ -118,11 +70,11 @@ struct DecodeShape {
   static constexpr int LPT = D / VEC;          // lanes per token row
   static_assert(LPT >= 1 && LPT <= 64 && (LPT & (LPT - 1)) == 0, "unsupported D/KV combination");
   static constexpr int TPI = 64 / LPT;         // token rows per load instruction
-  static constexpr int NI = NIO > 0 ? NIO : PA_DECODE_NI;  // K (and V) loads per lane per tile
+  static constexpr int NI = NIO > 0 ? NIO : 4;  // K (and V) loads per lane per tile
   static constexpr int TT = NI * TPI;          // tokens per wave tile
 };
 
-constexpr int kDecodeWaves = PA_DECODE_WAVES;
+constexpr int kDecodeWaves = 4;
 constexpr int kDecodeThreads = 64 * kDecodeWaves;
 constexpr int kBtChunk = 256;  // block-table entries staged in LDS at a time
 
@@ -159,8 +111,8 @@ template <typename KV, int D, int GC, int HP = 1, int DQ = 0>
 __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<KV, D, GC, HP, DQ>())))
 void decode_kernel(const DecodeParams p) {
   static_assert(DQ == 0 || (pair_types<KV>::value & (1 << DQ)), "the cache cannot provide q's pairs");
-  constexpr bool LAZY = PA_DECODE_LAZY && GC >= 2;
-  using Sh = DecodeShape<KV, D * HP, (GC == 1 && HP == 1) ? PA_DECODE_NI_MHA : 0>;
+  constexpr bool LAZY = GC >= 2;  // raise the softmax reference point only by more than 2^8
+  using Sh = DecodeShape<KV, D * HP, (GC == 1 && HP == 1) ? 2 : 0>;  // one unpacked MHA head: 2 loads per lane per tile (config 2 +0.8 % over 4)
   constexpr int VEC = Sh::VEC, LPT = Sh::LPT, TPI = Sh::TPI, NI = Sh::NI, TT = Sh::TT;
   // Packed P.V for GQA groups over fp16 or FP8 caches (V as fp16 pairs);
   // bf16 weights would be too coarse, so bf16 caches keep the fp32 path.
@@ -169,8 +121,8 @@ void decode_kernel(const DecodeParams p) {
   // exponential, shared across the quad.
   // The lane keeps its own head's row sum, shared across the quad once at the
   // end; with packed P.V the own weights are packed before they are shared.
-  constexpr bool PBC = PA_DECODE_PBCAST && LAZY && GC == 4 && D / VEC == 16;
-  constexpr bool PVP = PA_DECODE_PVDOT && LAZY && (Sh::NI % 2 == 0) && KV::kCode != kBF16 &&
+  constexpr bool PBC = LAZY && GC == 4 && D / VEC == 16;
+  constexpr bool PVP = LAZY && (Sh::NI % 2 == 0) && KV::kCode != kBF16 &&
                        ((pair_types<KV>::value >> kF16) & 1);
   constexpr int LPH = D / VEC;  // lanes per head's row
   constexpr int NW = kDecodeWaves;
@@ -183,7 +135,7 @@ void decode_kernel(const DecodeParams p) {
   // waves that are behind win issue and a CU's work-groups finish together:
   // config 2 6276 -> 6368 GB/s.  With more work-groups than slots (the
   // dispatcher backfills) or packed and GQA rows it measured 1-3 % slower.
-  constexpr bool PPRIO = PA_DECODE_PPRIO && GC == 1 && HP == 1;
+  constexpr bool PPRIO = GC == 1 && HP == 1;
 
   __shared__ int32_t s_bt[kBtChunk];
   __shared__ float s_acc[NW][GC][HP * D];
@@ -218,7 +170,7 @@ void decode_kernel(const DecodeParams p) {
   // every token row (12 heads on 8 XCDs); rotated, each XCD's requests cover
   // all slice offsets: config 2 6.17 -> 6.40 TB/s.  GQA and packed groups
   // measured slightly slower with it (-0.3 to -0.8 %) and keep the plain order.
-  if constexpr (PA_DECODE_ROT && GC == 1 && HP == 1) y = (y + (z * p.parts + part)) % units_y;
+  if constexpr (GC == 1 && HP == 1) y = (y + (z * p.parts + part)) % units_y;
   const int kvh = y / p.head_chunks;  // first KV head: kvh * HP
   const int hc = y - kvh * p.head_chunks;
   const int b = z / p.Sq;
@@ -239,7 +191,7 @@ void decode_kernel(const DecodeParams p) {
   // one memory round trip less at start-up (config 2 +0.2 %, FP8 config 3
   // +0.7 %).  Packed 16-bit MHA rows (config 5) measured -2.5 % with it and
   // keep the plain order.
-  constexpr bool BTPF = PA_DECODE_BTPF && !(GC == 1 && HP > 1 && KV::kCode != kFP8);
+  constexpr bool BTPF = !(GC == 1 && HP > 1 && KV::kCode != kFP8);
   const bool bt_early = BTPF && (p.part_tokens > 0 || part == 0);
   const int pg_early = p.part_tokens > 0 ? (int)(((int64_t)part * p.part_tokens) / p.BS) : 0;
   int32_t bt_pre = 0;
@@ -337,7 +289,7 @@ void decode_kernel(const DecodeParams p) {
   // of more than 2^31 blocks accepts every non-negative one, and a negative
   // id reads as >= 2^31.
   const uint32_t nb32 = nb > 0x80000000ull ? 0x80000000u : (uint32_t)nb;
-  constexpr bool SADDR = PA_DECODE_SADDR && (GC > 1 || KV::kCode == kFP8);
+  constexpr bool SADDR = GC > 1 || KV::kCode == kFP8;
 
   // One wave tile in flight: raw K/V rows of NI tokens per lane and which of
   // them are live (inside the partition, on a page with a valid block id).
@@ -369,8 +321,8 @@ void decode_kernel(const DecodeParams p) {
       bad |= (val[i] && !okb) ? 1 : 0;
       const uint32_t bb = okb ? (uint32_t)blk[i] : 0u;
       const uint32_t oo = okb ? (uint32_t)off[i] : 0u;
-      T.k[i] = load_raw<KV, PA_DECODE_NT>(kbase, (uint64_t)bb * k_sb + (oo * k_st + lane_off));
-      T.v[i] = load_raw<KV, PA_DECODE_NT>(vbase, (uint64_t)bb * v_sb + (oo * v_st + lane_off));
+      T.k[i] = load_raw<KV>(kbase, (uint64_t)bb * k_sb + (oo * k_st + lane_off));
+      T.v[i] = load_raw<KV>(vbase, (uint64_t)bb * v_sb + (oo * v_st + lane_off));
       live |= (val[i] && okb) ? (1u << i) : 0u;
     }
     T.live = live;
@@ -416,8 +368,8 @@ void decode_kernel(const DecodeParams p) {
       const uint32_t use = okb ? 1u : 0u;
       const uint64_t rk = (uint64_t)((uint32_t)blk * use) * k_sb + (uint32_t)off0[i] * use * k_st;
       const uint64_t rv = (uint64_t)((uint32_t)blk * use) * v_sb + (uint32_t)off0[i] * use * v_st;
-      T.k[i] = load_raw<KV, PA_DECODE_NT>(kbase + rk, ork);
-      T.v[i] = load_raw<KV, PA_DECODE_NT>(vbase + rv, orv);
+      T.k[i] = load_raw<KV>(kbase + rk, ork);
+      T.v[i] = load_raw<KV>(vbase + rv, orv);
       live |= (okb && ti + slot < ct1) ? (1u << i) : 0u;
     }
     T.live = live;
@@ -497,7 +449,7 @@ void decode_kernel(const DecodeParams p) {
     // two tokens (vlo: element 2w of tokens 2u and 2u+1, vhi: element 2w+1).
     float vf[PVP ? 1 : NI][PVP ? 1 : VEC];
     uint32_t vlo[PVP ? NI / 2 : 1][PVP ? VEC / 2 : 1], vhi[PVP ? NI / 2 : 1][PVP ? VEC / 2 : 1];
-    if constexpr (PVP && KV::kCode == kFP8 && PA_DECODE_F8PERM) {
+    if constexpr (PVP && KV::kCode == kFP8) {
       // FP8: interleave the two tokens' codes byte by byte first (two
       // v_perm_b32 per code word of each token), so that each packed
       // conversion yields a cross-token fp16 pair directly.
@@ -817,7 +769,7 @@ hipError_t launch_decode_one(const DecodeParams& p, int64_t blocks, hipStream_t 
   const auto kernel = decode_kernel<KV, D, GC, HP, DQ>;
   DecodeParams q = p;
   q.pprio = 0;
-  if constexpr (PA_DECODE_PPRIO && GC == 1 && HP == 1) {
+  if constexpr (GC == 1 && HP == 1) {
     static std::atomic<int64_t> cache[64];
     const int64_t res = decode_residency(kernel, cache);
     q.pprio = res > 0 && blocks <= res ? 1 : 0;
@@ -830,7 +782,7 @@ hipError_t launch_decode_one(const DecodeParams& p, int64_t blocks, hipStream_t 
 template <typename KV, int D, int GC, int HP = 1>
 hipError_t launch_decode_dg(const DecodeParams& p, hipStream_t stream) {
   const int64_t blocks = (int64_t)p.B * p.Sq * (p.HKV / HP) * p.head_chunks * p.parts;
-  constexpr int PTS = PA_DECODE_DOT2 ? pair_types<KV>::value : 0;
+  constexpr int PTS = pair_types<KV>::value;
   if constexpr ((PTS >> kF16) & 1) {
     if (p.q_dtype == kF16) return launch_decode_one<KV, D, GC, HP, kF16>(p, blocks, stream);
   }
@@ -844,21 +796,17 @@ template <typename KV, int D>
 hipError_t launch_decode_d(const DecodeParams& p, int gc, hipStream_t stream) {
   // Packed heads (the plan's choice) need K's and V's heads contiguous.
   if (gc == 1 && p.hp > 1 && p.k_sh == D && p.v_sh == D && p.HKV % p.hp == 0) {
-    if constexpr (D * KV::kBytes * 4 <= PA_PACK_ROW_BYTES && PA_PACK_MAX >= 4) {
+    if constexpr (D * KV::kBytes * 4 <= kPackRowBytes) {
       if (p.hp == 4) return launch_decode_dg<KV, D, 1, 4>(p, stream);
     }
-    if constexpr (D * KV::kBytes * 2 <= PA_PACK_ROW_BYTES) {
+    if constexpr (D * KV::kBytes * 2 <= kPackRowBytes) {
       if (p.hp == 2) return launch_decode_dg<KV, D, 1, 2>(p, stream);
     }
   }
-  // GQA groups of four with two (or four) KV heads per work-group (one head chunk).
-  if (gc == 4 && p.G == 4 && p.hp > 1 && p.k_sh == D && p.v_sh == D && p.HKV % p.hp == 0) {
-    if constexpr (KV::kBytes == 2 && D * KV::kBytes * 4 <= PA_PACK_GQA_ROW_BYTES && PA_PACK_GQA_MAX >= 4) {
-      if (p.hp == 4) return launch_decode_dg<KV, D, 4, 4>(p, stream);
-    }
-    if constexpr (KV::kBytes <= 2 && D * KV::kBytes * 2 <= PA_PACK_GQA_ROW_BYTES && PA_PACK_GQA_MAX >= 2) {
-      if (p.hp == 2) return launch_decode_dg<KV, D, 4, 2>(p, stream);
-    }
+  // GQA groups of four with two KV heads per work-group (one head chunk).
+  if (gc == 4 && p.G == 4 && p.hp == 2 && p.k_sh == D && p.v_sh == D && p.HKV % 2 == 0) {
+    static_assert(kPackGqaMax == 2, "GQA groups of four pack at most two KV heads");
+    if constexpr (KV::kBytes <= 2 && D * KV::kBytes * 2 <= kPackRowBytes) return launch_decode_dg<KV, D, 4, 2>(p, stream);
   }
   switch (gc) {
     case 1: return launch_decode_dg<KV, D, 1>(p, stream);

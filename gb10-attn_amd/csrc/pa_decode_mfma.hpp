@@ -91,11 +91,6 @@ __device__ inline int dm_vpos(int r, int cc) {
 
 constexpr float kDmLazy = 8.0f;  // raise the running max only past 2^8
 
-// K operand loads read half of a 128-byte line each (the other half is the
-// next k-step's), so they stay cacheable: the second access hits.
-#ifndef PA_DM_KNT
-#define PA_DM_KNT 0
-#endif
 
 // SQ: q may need the hi + lo split (q's dtype is not the cache's).  A
 // separate instance for q of the cache's dtype keeps the run-time test out of
@@ -242,7 +237,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(const DecodeParams p) 
     for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        T.k[mt][ks] = load16<PA_DM_KNT>(kbase + base_k[mt], k_lane + ks * 64);
+        T.k[mt][ks] = load16(kbase + base_k[mt], k_lane + ks * 64);  // cacheable: the other half of the line is the next k-step's
     }
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
@@ -432,8 +427,9 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(const DecodeParams p) 
 template <typename KV, int D, int GC>
 hipError_t launch_decode_mfma_dg(const DecodeParams& p, hipStream_t stream) {
   const int64_t blocks = (int64_t)p.B * p.Sq * p.HKV * p.head_chunks * p.parts;
-  note_launch("pa::decode_mfma_kernel<%s, %d, %d>", KV::kName, D, GC);
-  if (p.q_dtype == KV::kCode)
+  const bool sq = p.q_dtype != KV::kCode;
+  note_launch("pa::decode_mfma_kernel<%s, %d, %d, %s>", KV::kName, D, GC, sq ? "true" : "false");
+  if (!sq)
     hipLaunchKernelGGL((decode_mfma_kernel<KV, D, GC, false>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
   else
     hipLaunchKernelGGL((decode_mfma_kernel<KV, D, GC, true>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
@@ -451,7 +447,7 @@ bool decode_mfma_eligible(const DecodeParams& p, int gc) {
     return false;
   } else {
     const bool aligned = p.part_tokens > 0 ? p.part_tokens % 16 == 0 : p.parts == 1;
-    return gc >= 8 && p.Sq == 1 && p.BS % 16 == 0 && aligned && !p.cu_q && PA_DECODE_MFMA;
+    return gc >= 8 && p.Sq == 1 && p.BS % 16 == 0 && aligned && !p.cu_q;
   }
 }
 

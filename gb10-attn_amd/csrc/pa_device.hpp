@@ -143,21 +143,14 @@ __device__ inline float dot2(uint32_t a, uint32_t b, float c) {
 // accumulator.  Through the builtin the compiler materialises the zero with a
 // v_mov_b32 and then uses the accumulating v_dot2c form; the three-operand
 // form takes the zero as an inline constant.
-#ifndef PA_DOT2_FIRST_ASM
-#define PA_DOT2_FIRST_ASM 1
-#endif
 template <int PT>
 __device__ inline float dot2_first(uint32_t a, uint32_t b) {
-  if constexpr (PA_DOT2_FIRST_ASM) {
-    float r;
-    if constexpr (PT == kF16)
-      asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
-    else
-      asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-  } else {
-    return dot2<PT>(a, b, 0.0f);
-  }
+  float r;
+  if constexpr (PT == kF16)
+    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  else
+    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
 }
 template <int PT>
 __device__ inline uint32_t pack_pair_exact(float x, float y) {
@@ -173,20 +166,16 @@ struct pair_types { static constexpr int value = 0; };
 template <typename KV>
 struct pair_types<KV, std::void_t<decltype(KV::kPairs)>> { static constexpr int value = KV::kPairs; };
 
-template <int NT = 0>
 __device__ inline u32x4_t load16(const void* base, int64_t byte_off) {
-  const u32x4_t* ptr = reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(base) + byte_off);
-  if constexpr (NT) return __builtin_nontemporal_load(ptr);
-  return *ptr;
+  return *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(base) + byte_off);
 }
 
-// One lane's raw K/V load of a KV type (16 bytes, or 8 for FP8).
-template <typename KV, int NT = 0>
+// One lane's raw K/V load of a KV type (16 bytes, or 8 for FP8), with the
+// non-temporal (streaming) hint: each K/V row is read once per work-group.
+template <typename KV>
 __device__ inline typename KV::Raw load_raw(const void* base, int64_t byte_off) {
   using Raw = typename KV::Raw;
-  const Raw* ptr = reinterpret_cast<const Raw*>(reinterpret_cast<const char*>(base) + byte_off);
-  if constexpr (NT) return __builtin_nontemporal_load(ptr);
-  return *ptr;
+  return __builtin_nontemporal_load(reinterpret_cast<const Raw*>(reinterpret_cast<const char*>(base) + byte_off));
 }
 
 // ------------------------------------------------------- scalar element I/O --
@@ -312,24 +301,15 @@ __device__ inline float dpp(float v) {
 // keep without a source is never needed, and the mov form leaves it
 // undefined instead of materialising a zero (one v_mov_b32 per use).  dpp()
 // keeps the zero: the compiler folds that form into a following add.
-#ifndef PA_DPP_MOV
-#define PA_DPP_MOV 1
-#endif
 template <int CTRL>
 __device__ inline uint32_t dpp_quad_u(uint32_t v) {
   static_assert(CTRL >= 0 && CTRL <= 0xff, "quad permutations only");
-  if constexpr (PA_DPP_MOV)
-    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, false);
-  else
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, false);
 }
 template <int CTRL>
 __device__ inline float dpp_quad(float v) {
   static_assert(CTRL >= 0 && CTRL <= 0xff, "quad permutations only");
-  if constexpr (PA_DPP_MOV)
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
-  else
-    return dpp<CTRL>(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
 }
 
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]

@@ -115,12 +115,6 @@ __device__ inline void load8f(const void* q, int dtype, int64_t idx, float (&x)[
   }
 }
 
-#ifndef PA_PF_STORE
-#define PA_PF_STORE 1  // output stores: 1 four dims per store where the base allows it, 0 per element
-#endif
-#ifndef PA_PF_KB64
-#define PA_PF_KB64 64  // keys per tile at D <= 64
-#endif
 constexpr int kPfThreads = 256;   // 4 waves
 constexpr int kPfBtStage = 1024;  // block-table entries staged in LDS
 constexpr float kLazyRescale = 8.0f;  // raise the running max only past 2^8
@@ -157,7 +151,7 @@ template <int D>
 struct PfShape {
   static constexpr int QW = 32;                  // query rows per wave (one MFMA n-tile)
   static constexpr int QB = 4 * QW;              // query rows per work-group
-  static constexpr int KB = D <= 64 ? PA_PF_KB64 : D <= 128 ? 64 : 32;  // keys per tile
+  static constexpr int KB = D <= 128 ? 64 : 32;  // keys per tile
   static constexpr int MT = KB / 32;             // 32-key m-tiles of S^T
   static constexpr int KS = D / 16;              // 16-dim k-steps of Q.K^T
   static constexpr int DT = D / 32;              // 32-dim m-tiles of O^T
@@ -738,7 +732,7 @@ void prefill_mfma_kernel(const PrefillParams p) {
   // Slots 4j .. 4j+3 of m-tile dt are 4 consecutive dims: one 8-byte (16-bit
   // out) or 16-byte (fp32 out) store when the output base allows it.
   const uintptr_t oa = reinterpret_cast<uintptr_t>(p.out);
-  const bool vec = PA_PF_STORE != 0 && (p.out_dtype == kF32 ? (oa & 15) == 0 : (oa & 7) == 0);
+  const bool vec = (p.out_dtype == kF32 ? (oa & 15) == 0 : (oa & 7) == 0);
   if (!vec) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
@@ -815,13 +809,10 @@ static hipError_t launch_pf_q(const PrefillParams& p, hipStream_t stream) {
 }
 
 // Key-split mode when the plain grid (blocks of 128 query rows) has fewer
-// work-groups than CUs (PA_PF_SPLIT_BELOW per CU): chunks of a long context
+// work-groups than CUs: chunks of a long context
 // (the reference's 512-token chunk at context 2048: 192 work-groups, +19 %).
 // Above that, twice the tiles cost more than the shorter chains save
 // (config 4a, 768 work-groups: -17 %).
-#ifndef PA_PF_SPLIT_BELOW
-#define PA_PF_SPLIT_BELOW 1
-#endif
 template <typename KV, int D>
 static hipError_t launch_pf(const PrefillParams& p, hipStream_t stream) {
   if constexpr (PfShape<D>::MT == 2) {
@@ -829,7 +820,7 @@ static hipError_t launch_pf(const PrefillParams& p, hipStream_t stream) {
     int64_t cus = 0, per_cu = 0;
     residency(prefill_mfma_kernel<KV, D, false, false>, cache, &cus, &per_cu);
     const int64_t plain = (int64_t)p.B * p.H * ((p.S + PfShape<D>::QB - 1) / PfShape<D>::QB);
-    if (cus > 0 && plain < PA_PF_SPLIT_BELOW * cus)
+    if (cus > 0 && plain < cus)
       return p.q_split ? launch_pf_q<KV, D, true, true>(p, stream) : launch_pf_q<KV, D, false, true>(p, stream);
   }
   return p.q_split ? launch_pf_q<KV, D, true, false>(p, stream) : launch_pf_q<KV, D, false, false>(p, stream);

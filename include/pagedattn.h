@@ -191,7 +191,8 @@ int paged_attention_prefill_wmma(pa_tensor_t* out, const pa_tensor_t* q,
  * result is computed on K = k_cache * k_scale, V = v_cache * v_scale.  Any
  * decode KV type is accepted; with k_scale = v_scale = 1 it is
  * paged_attention_v3.  No reference counterpart: the reference has no FP8
- * cache (docs/REPORT.md:270 lists it as not done).  Workspace as for
+ * cache (docs/REPORT.md:270 lists it as not done).  Scales must be finite
+ * as float32, and so must scale * k_scale.  Workspace as for
  * paged_attention_v3 (same split plan). */
 int paged_attention_v3_scaled(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
                               const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
@@ -214,6 +215,18 @@ int paged_attention_v3_noalloc(pa_tensor_t* out, const pa_tensor_t* q, const pa_
                                const pa_tensor_t* context_lens, double scale, int64_t num_splits,
                                void* stream);
 
+/* paged_attention_prefill_wmma over a scaled cache (FP8 E4M3 pools written
+ * by pa_write_kv_scaled): K holds k / k_scale and V holds v / v_scale, so
+ * k_scale joins the softmax scale and v_scale multiplies the output rows.
+ * No reference counterpart (the reference has no FP8 path,
+ * docs/REPORT.md:270); the entry it extends is
+ * kernels/paged_attn_wmma.h:13-15.  Scales must be finite as float32, and
+ * so must scale * k_scale. */
+int paged_attention_prefill_wmma_scaled(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
+                                        const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
+                                        const pa_tensor_t* context_lens, double scale, double k_scale,
+                                        double v_scale, void* stream);
+
 /* Variable-length (mixed decode + prefill) batches on the MFMA path.  The
  * reference's prefill takes q [B, S, H, D] with one S for every sequence
  * (kernels/paged_attn_prefill.cu:62-64 trailing-chunk semantics); here
@@ -228,17 +241,6 @@ int paged_attention_v3_noalloc(pa_tensor_t* out, const pa_tensor_t* q, const pa_
  * row are computed by the decode kernel and the others by the MFMA prefill
  * kernel: two launches on the stream, told apart on the device (no host
  * synchronisation). */
-/* paged_attention_prefill_wmma over a scaled cache (FP8 E4M3 pools written
- * by pa_write_kv_scaled): K holds k / k_scale and V holds v / v_scale, so
- * k_scale joins the softmax scale and v_scale multiplies the output rows.
- * No reference counterpart (the reference has no FP8 path,
- * docs/REPORT.md:270); the entry it extends is
- * kernels/paged_attn_wmma.h:13-15.  Scales must be finite. */
-int paged_attention_prefill_wmma_scaled(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
-                                        const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
-                                        const pa_tensor_t* context_lens, double scale, double k_scale,
-                                        double v_scale, void* stream);
-
 int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
                                    const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
                                    const pa_tensor_t* context_lens, const pa_tensor_t* cu_seqlens_q,
@@ -248,7 +250,7 @@ int paged_attention_prefill_varlen(pa_tensor_t* out, const pa_tensor_t* q, const
  * by pa_write_kv_scaled): k_scale joins the softmax scale and v_scale
  * multiplies the output rows, in both kernels of the call.  No reference
  * counterpart (the reference has no FP8 path, docs/REPORT.md:270).  Scales
- * must be finite. */
+ * must be finite as float32, and so must scale * k_scale. */
 int paged_attention_prefill_varlen_scaled(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
                                           const pa_tensor_t* v_cache, const pa_tensor_t* block_tables,
                                           const pa_tensor_t* context_lens, const pa_tensor_t* cu_seqlens_q,
@@ -276,7 +278,7 @@ int pa_write_kv(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tensor_t* k
  * rounding), the quantised form paged_attention_v3_scaled reads back.  With
  * an FP8 E4M3 cache (also accepted by pa_write_kv, scale 1) each value is
  * rounded to nearest even and saturated at +-448 (infinities too), NaN is
- * stored as 0x7f.  Scales must be finite and nonzero.  The reference has no
+ * stored as 0x7f.  Scales must be finite and nonzero as float32.  The reference has no
  * FP8 path (docs/REPORT.md:270); the engine's write it extends is the one
  * pa_write_kv replaces (harness/repro_crash.py:52-58). */
 int pa_write_kv_scaled(pa_tensor_t* k_cache, pa_tensor_t* v_cache, const pa_tensor_t* key,

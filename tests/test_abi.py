@@ -271,9 +271,11 @@ def test_write_kv_shape_rejections(pa):
     assert rc == 2 and "multiples of 16 bytes" in err
 
 
-@pytest.mark.parametrize("ks,vs", [(0.0, 1.0), (1.0, float("inf")), (float("nan"), 1.0), (1e-50, 1.0)])
+@pytest.mark.parametrize("ks,vs", [(0.0, 1.0), (1.0, float("inf")), (float("nan"), 1.0), (1e-50, 1.0),
+                                   (1e39, 1.0), (1.0, -1e39)])
 def test_write_kv_scaled_rejects_bad_scales(pa, ks, vs):
-    """Scales must be finite and nonzero (as float32: 1e-50 rounds to 0); refused before any HIP call."""
+    """Scales must be finite and nonzero as float32 (1e-50 rounds to 0, 1e39 to inf); refused
+    before any HIP call."""
     a = write_args(pa, cdt=6)
     L = pa.lib()
     rc = L.pa_write_kv_scaled(C.byref(a["kc"]), C.byref(a["vc"]), C.byref(a["key"]), C.byref(a["val"]),
@@ -303,3 +305,30 @@ def test_torch_ops_load_with_reference_signatures(pa):
     with pytest.raises(RuntimeError, match="q must be on CUDA"):
         ops.paged_attention(torch.zeros(1, 4, 64), torch.zeros(1, 16, 4, 64), torch.zeros(1, 16, 4, 64),
                             torch.zeros(1, 1, dtype=torch.int32), torch.ones(1, dtype=torch.int32), 0.1)
+
+
+@pytest.mark.parametrize("fn,extra", [
+    ("paged_attention_v3_scaled", lambda ks, vs: (ks, vs, 4, None, 0, None)),
+    ("paged_attention_prefill_wmma_scaled", lambda ks, vs: (ks, vs, None)),
+])
+@pytest.mark.parametrize("scale,ks,vs,msg", [
+    (0.1, 1e39, 1.0, "k_scale and v_scale must be finite"),
+    (0.1, 1.0, -1e39, "k_scale and v_scale must be finite"),
+    (0.1, float("nan"), 1.0, "k_scale and v_scale must be finite"),
+    (1e30, 1e10, 1.0, "must be finite"),   # each finite, the folded softmax scale is not (as float32)
+])
+def test_scaled_entries_reject_scales_past_float32(pa, fn, extra, scale, ks, vs, msg):
+    """The kernels take the scales as float32: a finite double that overflows it is refused."""
+    a = args(pa, prefill="prefill" in fn, qdt=F16, odt=F16)
+    if "prefill" in fn:
+        a["q"] = T(pa, [2, 3, 4, 64], F16)
+    rc, err = call(pa, fn, a, scale=scale, extra=extra(ks, vs))
+    assert rc == 1 and msg in err, (rc, err)
+
+
+@pytest.mark.parametrize("fn", ["paged_attention", "paged_attention_v3", "paged_attention_prefill_wmma"])
+def test_scale_past_float32_rejected(pa, fn):
+    """scale * log2(e) must be finite as float32 (the kernels' softmax scale)."""
+    a = args(pa, prefill="prefill" in fn, qdt=F16, odt=F16, kvdt=F16)
+    rc, err = call(pa, fn, a, scale=3e38, extra=ENTRY_EXTRA[fn])
+    assert rc == 1 and "scale must be finite" in err, (rc, err)

@@ -257,14 +257,16 @@ def test_varlen_malformed_ranges_and_max_q_len(pa, dev):
             close(got[5:5 + 32], want[:32])
 
 
-@pytest.mark.parametrize("kv,D", [("f16", 64), ("bf16", 128)])
-def test_varlen_all_single_rows(pa, dev, kv, D):
+@pytest.mark.parametrize("kv,D,H,HKV", [("f16", 64, 8, 2), ("bf16", 128, 8, 2), ("bf16", 128, 16, 2)])
+def test_varlen_all_single_rows(pa, dev, kv, D, H, HKV):
     """A batch of decode steps (max_q_len = 1), served by the decode kernel in
     the varlen call: sequences of one row match the oracle's decode, one with
-    an empty context is zeros, and a sequence without rows writes nothing."""
+    an empty context is zeros, and a sequence without rows writes nothing.
+    GQA groups of 4 and of 8 (the latter on the vector-ALU decode kernel: the
+    matrix-core decode does not serve varlen calls)."""
     qlens = [1, 1, 0, 1, 1]
     ctxs = [300, 17, 40, 1, 900]
-    H, HKV, BS = 8, 2, 16
+    BS = 16
     inp, q, q32, cu = varlen_case(qlens, ctxs, H, HKV, D, BS, seed=D + 2, kv=kv, qt=kv)
     ctx = inp["ctx"].copy()
     ctx[3] = 0
@@ -274,13 +276,32 @@ def test_varlen_all_single_rows(pa, dev, kv, D):
                                       torch.from_numpy(inp["bt"]).to(dev), torch.from_numpy(ctx).to(dev),
                                       torch.from_numpy(cu).to(dev), 1, 1.0 / np.sqrt(D), out=out)
     launched = pa.last_launch()
-    assert "decode_kernel" in launched, launched
+    assert "decode_kernel" in launched and "decode_mfma_kernel" not in launched, launched
+    assert f"{D}, {H // HKV}, 1, " in launched, launched  # one KV head's group per work-group
     got = to_host(out)
     for b in (0, 1, 4):
         rows = slice(cu[b], cu[b + 1])
         close(got[rows], oracle.decode(q32[rows], inp["k"], inp["v"], inp["bt"][b:b + 1], ctx[b:b + 1],
                                        1.0 / np.sqrt(D), kv))
     assert np.all(got[cu[3]:cu[4]] == 0.0)
+
+
+def test_varlen_single_rows_packed_gqa4(pa, dev):
+    """Enough one-row sequences of a GQA-4 bf16 model that the decode launch of
+    the varlen call packs two KV heads per work-group (groups of four, quad-
+    shared); every row against the oracle's decode."""
+    B, H, HKV, D, BS = 200, 32, 8, 128, 16
+    rng = np.random.default_rng(50)
+    ctxs = [int(c) for c in rng.integers(1, 300, B)]
+    qlens = [1] * B
+    inp, q, q32, cu = varlen_case(qlens, ctxs, H, HKV, D, BS, seed=50, kv="bf16", qt="bf16")
+    got = to_host(pa.paged_attention_prefill_varlen(
+        to_dev(q, "bf16", dev), to_dev(inp["k"], "bf16", dev), to_dev(inp["v"], "bf16", dev),
+        torch.from_numpy(inp["bt"]).to(dev), torch.from_numpy(inp["ctx"]).to(dev),
+        torch.from_numpy(cu).to(dev), 1, 1.0 / np.sqrt(D)))
+    launched = pa.last_launch()
+    assert "decode_kernel<pa::KvBF16, 128, 4, 2, " in launched, launched
+    close(got, oracle.decode(q32, inp["k"], inp["v"], inp["bt"], inp["ctx"], 1.0 / np.sqrt(D), "bf16"))
 
 
 @pytest.mark.parametrize("kv,qt", [("f16", "f16"), ("bf16", "bf16"), ("f16", "f32"), ("bf16", "f32")])

@@ -2,7 +2,8 @@
 paged_attention_v3 with a caller workspace, bit for bit (same plan, same
 kernels), on two calls in a row whose second input is smaller, and a clear
 PA_ERR_WORKSPACE (with the output untouched) when a split needs more than the
-fixed scratch."""
+fixed scratch; and the entry recorded into a HIP graph and replayed on
+changed inputs."""
 import ctypes as C
 
 import numpy as np
@@ -70,3 +71,40 @@ def test_noalloc_rejects_oversized_split(pa, dev):
     assert "paged_attention_v3_noalloc" in pa.last_error() and str(need) in pa.last_error()
     torch.cuda.synchronize()
     assert bool((out == 7.0).all())
+
+
+def test_noalloc_graph_capture_and_replay(pa, dev):
+    """paged_attention_v3_noalloc recorded into a HIP graph (after one eager
+    call on the capture stream, which does the per-device set-up: scratch
+    address, CU count), replayed three times after q and context_lens change
+    in place, with eager work and synchronisation between replays: every
+    replay equals eager paged_attention_v3 with a workspace, bit for bit."""
+    inp = decode_case(6, 32, 8, 128, 16, [900, 4000, 17, 2500, 1, 3100], seed=41, kv="bf16", q="bf16")
+    q, k, v, bt, ctx = dev_inputs(inp, dev)
+    scale = 1.0 / np.sqrt(128)
+    assert pa.workspace_size(q, k, bt, 0) > 0, "the auto plan must split (the scratch is in use)"
+    out = torch.empty_like(q)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        assert _noalloc(pa, out, q, k, v, bt, ctx, scale, 0) == 0, pa.last_error()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = _noalloc(pa, out, q, k, v, bt, ctx, scale, 0)
+    assert rc == 0, pa.last_error()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(42)
+    maxctx = bt.shape[1] * k.shape[1]
+    for i in range(3):
+        print(f"noalloc graph replay {i}", flush=True)
+        q.copy_(torch.randn(q.shape, generator=gen, device=dev).to(q.dtype))
+        ctx.copy_(torch.randint(0, maxctx + 1, ctx.shape, generator=gen, device=dev).to(ctx.dtype))
+        ref = torch.empty_like(out)
+        _with_workspace(pa, ref, q, k, v, bt, ctx, scale, 0)
+        out.fill_(7.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), i
