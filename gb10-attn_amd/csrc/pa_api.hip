@@ -169,6 +169,10 @@ int scratch_address(void** ptr) {
 // kernel serves the group (finer balance for ragged batches, config 3: +4 %;
 // the matrix-core kernel, groups of 8+, amortises its set-up over the longer
 // one).
+// Longest explicit partition (tokens, at the block table's capacity) served
+// in the wave-partition mode.
+constexpr int64_t kWavePartTokens = 256;
+
 struct PlanKnobs {
   int64_t wgs_per_cu = 3;
   int64_t min_part = 256;
@@ -445,6 +449,12 @@ int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const p
     if ((rc = device_cu_count(&cus))) return rc;
     a.p.hp = pack_for(a.p, dtype_bytes(a.kv_dtype), plan.parts, cus);
   }
+  // Explicit splits into short chunks (the reference's own count at long
+  // contexts: 64 splits of 32 tokens at ctx 2048) run in the wave-partition
+  // mode: one work-group per kDecodeWaves consecutive partitions, one per wave,
+  // each written as its own partials.
+  const int64_t maxctx = (int64_t)a.p.MB * a.p.BS;
+  a.p.wave_parts = num_splits > 0 && !plan.direct && (maxctx + plan.parts - 1) / plan.parts <= kWavePartTokens;
   if (!plan.direct) bind_workspace(&a.p, ws, plan);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (phases & kPartition) {

@@ -61,6 +61,8 @@ struct DecodeParams {
   int32_t direct;       // 1: one partition, every WG writes the normalised output
   int32_t hp;           // KV heads per work-group (head packing: MHA, or GQA groups of four); <= 1: one
   int32_t pprio;        // 1: the whole grid is resident at once; waves lower their priority as they progress
+  int32_t wave_parts;   // 1: each wave serves a partition of its own; a work-group covers kDecodeWaves
+                        // consecutive partitions (explicit splits into short chunks)
   FastDiv bs_div;
   float qscale;         // scale * k_scale * log2(e): scores come out in log2 units
   float vscale;         // v_scale (FP8 caches): applied to the weighted V sum

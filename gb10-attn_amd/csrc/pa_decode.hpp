@@ -157,9 +157,18 @@ void decode_kernel(const DecodeParams p) {
   int id = blockIdx.x;
   int y = id % units_y;
   id /= units_y;
-  int part, z;
+  // Wave-partition mode: work-group `grp` serves partitions grp * NW + w,
+  // one per wave w (short chunks: one partition is a few wave tiles, and a
+  // work-group per partition would pay its start-up for each).
+  const bool wpm = p.wave_parts != 0;
+  const int ngrp = (p.parts + NW - 1) / NW;
+  int part, z, grp = 0;
   if (compact_grid(p)) {
     if (!compact_unit(p, id, lane, z, part)) return;  // work-group uniform
+  } else if (wpm) {
+    grp = id % ngrp;
+    z = id / ngrp;
+    part = grp * NW + wave;
   } else {
     part = id % p.parts;
     z = id / p.parts;
@@ -170,7 +179,7 @@ void decode_kernel(const DecodeParams p) {
   // every token row (12 heads on 8 XCDs); rotated, each XCD's requests cover
   // all slice offsets: config 2 6.17 -> 6.40 TB/s.  GQA and packed groups
   // measured slightly slower with it (-0.3 to -0.8 %) and keep the plain order.
-  if constexpr (GC == 1 && HP == 1) y = (y + (z * p.parts + part)) % units_y;
+  if constexpr (GC == 1 && HP == 1) y = (y + (wpm ? z * ngrp + grp : z * p.parts + part)) % units_y;
   const int kvh = y / p.head_chunks;  // first KV head: kvh * HP
   const int hc = y - kvh * p.head_chunks;
   const int b = z / p.Sq;
@@ -186,14 +195,18 @@ void decode_kernel(const DecodeParams p) {
   }
 
   // The first block-table chunk of the partition is fetched before the
-  // context length has arrived when its first page is known without it (the
-  // first partition, or fixed-length partitions): the K/V loads then wait for
-  // one memory round trip less at start-up (config 2 +0.2 %, FP8 config 3
-  // +0.7 %).  Packed 16-bit MHA rows (config 5) measured -2.5 % with it and
-  // keep the plain order.
-  constexpr bool BTPF = !(GC == 1 && HP > 1 && KV::kCode != kFP8);
-  const bool bt_early = BTPF && (p.part_tokens > 0 || part == 0);
-  const int pg_early = p.part_tokens > 0 ? (int)(((int64_t)part * p.part_tokens) / p.BS) : 0;
+  // context length has arrived: the K/V loads then wait for one memory round
+  // trip less at start-up (config 2 +0.2 %, FP8 config 3 +0.7 %).  Fixed-
+  // length partitions know their first page; partitions of ceil(ctx / parts)
+  // tokens take it from a context that fills the block table (maxctx), and
+  // the staging below uses the prefetched entries only if that was right.
+  // Packed 16-bit MHA rows (config 5) measured -2.5 % with it and keep the
+  // plain order, except in the wave-partition mode, whose short partitions
+  // are mostly start-up.
+  const bool bt_early = !(GC == 1 && HP > 1 && KV::kCode != kFP8) || wpm;  // work-group uniform
+  const int64_t chunk_guess = ((int64_t)p.MB * p.BS + p.parts - 1) / p.parts;
+  const int pg_early = p.part_tokens > 0 ? (int)(((int64_t)part * p.part_tokens) / p.BS)
+                                         : (int)(((wpm ? (int64_t)grp * NW : (int64_t)part) * chunk_guess) / p.BS);
   int32_t bt_pre = 0;
   if (bt_early && pg_early + (int)threadIdx.x < p.MB)
     bt_pre = p.block_tables[(int64_t)b * p.bt_stride + pg_early + threadIdx.x];
@@ -220,16 +233,22 @@ void decode_kernel(const DecodeParams p) {
     }
     return;
   }
-  if (part >= nparts) return;
+  if (wpm ? grp * NW >= nparts : part >= nparts) return;  // work-group uniform
 
-  int t0, t1;
+  // This wave's tokens [t0, t1); the work-group's [T0, T1) (wave-partition
+  // mode: its waves' partitions together; otherwise the same range).
+  int t0, t1, T0, T1;
   if (fixed) {
     t0 = part * p.part_tokens;
     t1 = min(t0 + p.part_tokens, ctx);
+    T0 = t0;
+    T1 = t1;
   } else {
     const int chunk = (ctx + p.parts - 1) / p.parts;  // kernels/paged_attn_v3.cu:65-68
-    t0 = part * chunk;
+    t0 = min(part * chunk, ctx);
     t1 = min(t0 + chunk, ctx);
+    T0 = wpm ? min(grp * NW * chunk, ctx) : t0;
+    T1 = wpm ? min(T0 + NW * chunk, ctx) : t1;
   }
 
   // This lane's slice of q for the GC heads, pre-scaled into log2 units.
@@ -601,13 +620,13 @@ void decode_kernel(const DecodeParams p) {
   };
 
   const bool fast = (p.BS % TPI) == 0 && (t0 % TPI) == 0;
-  if (t0 < t1) {
-    const int pg0 = (int)fastdiv((uint32_t)t0, p.bs_div);
-    const int pg1 = (int)fastdiv((uint32_t)(t1 - 1), p.bs_div) + 1;
+  if (T0 < T1) {
+    const int pg0 = (int)fastdiv((uint32_t)T0, p.bs_div);
+    const int pg1 = (int)fastdiv((uint32_t)(T1 - 1), p.bs_div) + 1;
     for (int cp = pg0; cp < pg1; cp += kBtChunk) {
       const int np = min(kBtChunk, pg1 - cp);
       __syncthreads();
-      if (bt_early && cp == pg0) {
+      if (bt_early && cp == pg0 && pg0 == pg_early) {
         static_assert(kBtChunk <= kDecodeThreads, "one prefetched entry per thread");
         if ((int)threadIdx.x < np) s_bt[threadIdx.x] = bt_pre;
       } else {
@@ -622,8 +641,8 @@ void decode_kernel(const DecodeParams p) {
       // path reaching a consume has the same loads outstanding and the wait
       // before it covers only the current tile.
       auto sweep = [&](auto&& iss) {
-        constexpr int kStep = NW * TT;
-        const int first = ct0 + wave * TT;
+        const int kStep = wpm ? TT : NW * TT;  // this wave's tiles: its own partition's, or every NW-th
+        const int first = wpm ? ct0 : ct0 + wave * TT;
         if (first < ct1) {
           // Counted, branch-free body: tile j+1 is issued before tile j is
           // consumed.  Every entry of the loop header has exactly one tile
@@ -699,6 +718,26 @@ void decode_kernel(const DecodeParams p) {
       }
       m[g] = mn;
     }
+  }
+  if (wpm) {
+    // This wave's partition complete: its partials straight from the lanes
+    // of slot 0 (dims dsub * VEC .. of head hl), m and l from those of dsub 0.
+    const bool wbad = __builtin_amdgcn_ballot_w64(bad != 0) != 0;
+    if (slot == 0 && part < nparts) {
+#pragma unroll
+      for (int g = 0; g < GC; ++g) {
+        if (g0 + g >= p.G) continue;
+        const int h = (kvh * HP + hl) * p.G + g0 + g;
+        const int64_t pidx = ((int64_t)b * p.H + h) * p.parts + part;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) p.ws_acc[pidx * D + dsub * VEC + e] = acc[g][e] * p.vscale;
+        if (dsub == 0) {
+          p.ws_m[pidx] = m[g];
+          p.ws_l[pidx] = wbad ? __builtin_nanf("") : l[g];
+        }
+      }
+    }
+    return;
   }
   if (slot == 0) {
 #pragma unroll
@@ -781,7 +820,8 @@ hipError_t launch_decode_one(const DecodeParams& p, int64_t blocks, hipStream_t 
 
 template <typename KV, int D, int GC, int HP = 1>
 hipError_t launch_decode_dg(const DecodeParams& p, hipStream_t stream) {
-  const int64_t blocks = (int64_t)p.B * p.Sq * (p.HKV / HP) * p.head_chunks * p.parts;
+  const int64_t groups = p.wave_parts ? (p.parts + kDecodeWaves - 1) / kDecodeWaves : p.parts;
+  const int64_t blocks = (int64_t)p.B * p.Sq * (p.HKV / HP) * p.head_chunks * groups;
   constexpr int PTS = pair_types<KV>::value;
   if constexpr ((PTS >> kF16) & 1) {
     if (p.q_dtype == kF16) return launch_decode_one<KV, D, GC, HP, kF16>(p, blocks, stream);

@@ -1,9 +1,15 @@
 // pa_reduce.hip -- log-sum-exp reduce of the context-split partials, the
 // separate second launch of the split decode (kernels/paged_attn_v3.cu:128-166):
 //   M = max_s m_s,  w_s = 2^(m_s - M),  out = sum_s w_s acc_s / sum_s w_s l_s
-// (m in log2 units).  One wave per (sequence, query head): lanes load the
-// partition states in parallel, reduce them with cross-lane operations, then
-// stream the D-wide partial rows with the weights broadcast from SGPRs.
+// (m in log2 units).  One wave per (sequence, query head).  Lane (r, c)
+// covers dims 4c .. 4c + 3 of the partial rows (LR = D / 4 lanes per row) for
+// every RI-th partition (RI = 64 / LR rows per load instruction), so a round
+// of NL loads per lane reads NL * RI whole rows at once; the partition states
+// sit one per lane, and each weight reaches the lanes that read its row by a
+// lane permute.  The kernel is latency-bound (a few MB of partials): the
+// context length, the first 64 partition states and the first round of rows
+// are loaded in one round trip, and a split of up to 64 partitions (D <= 64;
+// 32 at D = 128, 16 at D = 256) needs no other.
 #include "pa_device.hpp"
 
 namespace pa {
@@ -24,31 +30,34 @@ __device__ inline float wave_sum(float v) {
 
 template <int D>
 __global__ __launch_bounds__(64 * kReduceWaves) void reduce_kernel(const ReduceParams p) {
-  constexpr int DPL = (D + 63) / 64;  // dims per lane
-  constexpr int CH = 8;               // partial rows whose loads are issued together
+  constexpr int LR = D / 4;                  // lanes per partial row
+  constexpr int RI = 64 / LR;                // rows per load instruction
+  constexpr int NL = 64 / RI < 16 ? 64 / RI : 16;  // loads per lane per round
+  constexpr int PR = NL * RI;                // partitions per round (divides 64)
+  static_assert(LR >= 1 && LR <= 64 && 64 % PR == 0, "unsupported head_dim");
   const int lane = threadIdx.x & 63;
+  const int r = lane / LR, c = lane % LR;
   const int64_t f = (int64_t)blockIdx.x * kReduceWaves + (threadIdx.x >> 6);
   if (f >= (int64_t)p.B * p.H) return;
   const int b = (int)(f / p.H);
   const int P = p.parts;
   const int64_t base = f * P;
 
-  // The kernel is latency-bound (a few hundred KB of partials), so the
-  // context length, the partition states and the first CH partial rows are
-  // loaded in one round trip, before the partition count is known.  Entries
-  // past the count (never written by this call's partition pass) are loaded
-  // -- they lie inside the workspace -- but only ever selected away.
+  // One round trip: the context length, partition states 0..63, the first
+  // round of rows (partitions past this call's count are not loaded).
   const int ctx = p.context_lens[b];
   float mv = lane < P ? p.ws_m[base + lane] : kNegBig;
   float lv = lane < P ? p.ws_l[base + lane] : 0.0f;
-  float rows[CH][DPL];
+  float4_t rows[NL];
+  auto load_rows = [&](int s0, int lim) {
 #pragma unroll
-  for (int i = 0; i < CH; ++i)
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const int d = lane + 64 * j;
-      rows[i][j] = (i < P && d < D) ? p.ws_acc[(base + i) * D + d] : 0.0f;
+    for (int i = 0; i < NL; ++i) {
+      const int s = s0 + i * RI + r;
+      rows[i] = s < lim ? *reinterpret_cast<const float4_t*>(p.ws_acc + (base + s) * D + 4 * c)
+                        : float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
+  };
+  load_rows(0, P);
 
   const int maxctx = p.MB * p.BS;
   const bool fixed = p.part_tokens > 0;
@@ -61,10 +70,9 @@ __global__ __launch_bounds__(64 * kReduceWaves) void reduce_kernel(const ReduceP
   } else {
     if (!ok) {
       const float fillv = ctx <= 0 ? 0.0f : __builtin_nanf("");
+      if (r == 0) {
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        const int d = lane + 64 * j;
-        if (d < D) store_elem(p.out, p.out_dtype, f * D + d, fillv);
+        for (int e = 0; e < 4; ++e) store_elem(p.out, p.out_dtype, f * D + 4 * c + e, fillv);
       }
       return;
     }
@@ -79,59 +87,39 @@ __global__ __launch_bounds__(64 * kReduceWaves) void reduce_kernel(const ReduceP
   }
   M = wave_max(M);
 
-  // Partitions 0..63: weights in their lanes, rows from registers (first CH)
-  // or loaded CH at a time.
-  float w = lane < n ? fast_exp2(mv - M) : 0.0f;
-  float L = lane < n ? w * lv : 0.0f;
-  float acc[DPL];
-#pragma unroll
-  for (int j = 0; j < DPL; ++j) acc[j] = 0.0f;
-  auto add_rows = [&](int s0, const float (&r)[CH][DPL], float wl) {
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), i));
-      if (s0 + i < n) {
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) acc[j] = fmaf(wi, r[i][j], acc[j]);
-      }
+  float4_t acc = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float L = 0.0f;
+  for (int w0 = 0; w0 < n; w0 += 64) {  // windows of 64 partitions: their weights in the lanes
+    if (w0 > 0) {
+      const int s = w0 + lane;
+      mv = s < n ? p.ws_m[base + s] : kNegBig;
+      lv = s < n ? p.ws_l[base + s] : 0.0f;
     }
-  };
-  auto load_rows = [&](int s0, float (&r)[CH][DPL]) {
+    const float w = w0 + lane < n ? fast_exp2(mv - M) : 0.0f;
+    L += w0 + lane < n ? w * lv : 0.0f;
+    for (int k0 = 0; k0 < 64 && w0 + k0 < n; k0 += PR) {
+      if (w0 + k0 > 0) load_rows(w0 + k0, n);
 #pragma unroll
-    for (int i = 0; i < CH; ++i)
+      for (int i = 0; i < NL; ++i) {
+        const int j = k0 + i * RI + r;  // this row's partition within the window
+        const float wi = __shfl(w, j, 64);
+        // Rows past the count may hold anything (0 * NaN is NaN): selected away.
+        const float4_t x = w0 + j < n ? rows[i] : float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        const int d = lane + 64 * j;
-        r[i][j] = (s0 + i < n && d < D) ? p.ws_acc[(base + s0 + i) * D + d] : 0.0f;
-      }
-  };
-  add_rows(0, rows, w);
-  for (int s0 = CH; s0 < n; s0 += CH) {
-    if ((s0 & 63) == 0) {  // next 64 partitions: their weights into the lanes
-      const int s = s0 + lane;
-      const float m2 = s < n ? p.ws_m[base + s] : kNegBig;
-      const float l2 = s < n ? p.ws_l[base + s] : 0.0f;
-      w = s < n ? fast_exp2(m2 - M) : 0.0f;
-      L += s < n ? w * l2 : 0.0f;
-    }
-    load_rows(s0, rows);
-    // Lane i of the 64-lane window holds the weight of partition (s0 & ~63) + i.
-    const int wl0 = s0 & 63;
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const float wi = __builtin_bit_cast(
-          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), wl0 + i));
-      if (s0 + i < n) {
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) acc[j] = fmaf(wi, rows[i][j], acc[j]);
+        for (int e = 0; e < 4; ++e) acc[e] = fmaf(wi, x[e], acc[e]);
       }
     }
   }
-  L = wave_sum(L);
+  // Sum the RI row groups (lanes c, c + LR, ...), then the row sums.
 #pragma unroll
-  for (int j = 0; j < DPL; ++j) {
-    const int d = lane + 64 * j;
-    if (d < D) store_elem(p.out, p.out_dtype, f * D + d, acc[j] / L);
+  for (int off = LR; off < 64; off <<= 1) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], off, 64);
+  }
+  L = wave_sum(L);
+  if (r == 0) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) store_elem(p.out, p.out_dtype, f * D + 4 * c + e, acc[e] / L);
   }
 }
 
