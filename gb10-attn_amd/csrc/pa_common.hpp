@@ -130,6 +130,8 @@ struct WriteParams {
   float k_rcp, v_rcp;      // 1 / k_scale, 1 / v_scale rounded to nearest (fp32)
   int32_t k_fast, v_fast;  // |k_rcp|, |v_rcp| in [2^-60, 2^60]: the reciprocal-based division applies
   FastDiv bs_div;
+  FastDiv chunk_div, hkv_div;  // D / 8 and HKV (work item -> token, head, chunk)
+  int32_t t_base;              // first token of this launch (large writes take several)
 };
 
 // Records the kernel instance a launcher is about to dispatch, as profilers
