@@ -145,21 +145,20 @@ class DecodeWorkload:
             raise RuntimeError(self.pa.last_error())
 
 
-class SweepWorkload(DecodeWorkload):
-    """GPT-2 decode (H=12, D=64, BS=16, fp16) at batch B and context ctx through
-    paged_attention_v3 with the library's plan: the small-batch / short-context
-    cold sweep of the reference (harness/gb10_burst.sh:103-116).  One shared
-    pool of at least 4x the 256 MB Infinity Cache, cut into disjoint block-table
-    sets used in rotation, one per step (the reference's --cold-pools)."""
+class ScatteredWorkload(DecodeWorkload):
+    """GPT-2 decode (H=12, D=64, BS=16, fp16) at batch B and context ctx over ONE
+    shared pool cut into disjoint block-table sets used in rotation, one per
+    step, each set's pages a random draw from the whole pool: the layout of a
+    serving cache whose free list has been shuffled by many requests."""
 
-    def __init__(self, pa, pool, *, B, ctx, seed):
+    def __init__(self, pa, pool, *, B, ctx, seed, name, max_sets=4096):
         k, v = pool
         BS = k.shape[1]
         per_call = B * (-(-ctx // BS))
-        sets = max(1, min(k.shape[0] // per_call, 4096))
-        self._sets, self._per_call = sets, per_call
+        sets = max(1, min(k.shape[0] // per_call, max_sets))
+        self._sets, self._per_call, self._pool_blocks = sets, per_call, k.shape[0]
         super().__init__(pa, B=B, H=12, HKV=12, D=64, BS=BS, ctx=[ctx] * B, dtype=torch.float16, pools=sets,
-                         seed=seed, name=f"sweep_b{B}_c{ctx}", pool_tensor=lambda p: (k, v))
+                         seed=seed, name=name, pool_tensor=lambda p: (k, v))
 
     def _tables(self, rng, nbp, nb, B, pages, p):
         if p == 0:
@@ -167,7 +166,22 @@ class SweepWorkload(DecodeWorkload):
         return self._perm[p * nb:(p + 1) * nb]
 
     def footprint_gb(self):
+        """Bytes of the distinct pages the rotation reads (K and V)."""
         return self._sets * self._per_call * 2 * self.BS * self.HKV * self.D * 2 / 1e9
+
+    def pool_gb(self):
+        return self._pool_blocks * 2 * self.BS * self.HKV * self.D * 2 / 1e9
+
+
+class SweepWorkload(ScatteredWorkload):
+    """The small-batch / short-context cold sweep of the reference
+    (harness/gb10_burst.sh:103-116) through paged_attention_v3 with the
+    library's plan: one shared pool of at least 4x the 256 MB Infinity Cache,
+    cut into disjoint block-table sets used in rotation (the reference's
+    --cold-pools)."""
+
+    def __init__(self, pa, pool, *, B, ctx, seed):
+        super().__init__(pa, pool, B=B, ctx=ctx, seed=seed, name=f"sweep_b{B}_c{ctx}")
 
 
 # ----------------------------------------------------------------- prefill --
@@ -794,6 +808,21 @@ def make_c2(pa, pools):
                           pools=pools, seed=2, name="decode_c2")
 
 
+def make_c2_scattered(pa, sets):
+    """Config 2 over one pool of `sets` x the batch's 8192 pages (at least 4x:
+    2.4 GB of K and V at 6 sets), each step's block tables a disjoint random
+    draw from the whole pool: the same bytes per step and the same number of
+    rotated sets as the headline, whose pools each hold exactly one batch."""
+    sets = max(4, sets)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(22)
+    nb = sets * 64 * (2048 // 16)
+    k = torch.randn((nb, 16, 12, 64), generator=g, device=dev, dtype=torch.float32).half()
+    v = torch.randn((nb, 16, 12, 64), generator=g, device=dev, dtype=torch.float32).half()
+    return ScatteredWorkload(pa, (k, v), B=64, ctx=2048, seed=2, name="decode_c2_scattered")
+
+
 def make_c2_fp32io(pa, pools):
     """Config 2 with the reference's operator dtypes: fp32 q and fp32 out over
     the fp16 cache (kernels/paged_attn_v3.cu:40,130,220-221)."""
@@ -1145,7 +1174,7 @@ def main():
     ap.add_argument("--pools", type=int, default=6, help="rotated KV pools (config 2)")
     ap.add_argument("--workload", default="decode_c2",
                     choices=["decode_c2", "decode_c2_fp32io", "decode_c3", "decode_c5", "decode_c2_fp8", "decode_c3_fp8", "decode_gqa8",
-                             "decode_c2_split", "sweep", "prefill_c4a", "prefill_c4b", "prefill_ref_chunk", "prefill_c4b_fp8",
+                             "decode_c2_split", "decode_c2_scattered", "sweep", "prefill_c4a", "prefill_c4b", "prefill_ref_chunk", "prefill_c4b_fp8",
                              "write_kv_c4a", "write_kv_c4b", "write_kv_c4b_fp8", "call_overhead", "mixed_c2", "copy_calib"],
                     help="with --only: run just this workload's kernel loop (for profiling)")
     ap.add_argument("--only", action="store_true", help="time only --workload, print its record")
@@ -1194,6 +1223,7 @@ def main():
         else:
             work = {"decode_c2": lambda: make_c2(pa, args.pools), "decode_c3": lambda: make_c3(pa, 2),
                     "decode_c2_fp32io": lambda: make_c2_fp32io(pa, args.pools),
+                    "decode_c2_scattered": lambda: make_c2_scattered(pa, args.pools),
                     "decode_c2_fp8": lambda: make_c2_fp8(pa, args.pools),
                     "decode_c3_fp8": lambda: make_c3_fp8(pa, 2),
                     "decode_gqa8": lambda: make_gqa8(pa, 2),
@@ -1254,7 +1284,8 @@ def main():
     if not args.no_also:
         log("bench: config 2 through the explicit split + LSE reduce")
         also += c2_split_records(pa, args.pools, max(20, args.steps // 4))
-        for make in (lambda: make_c2_fp32io(pa, args.pools), lambda: make_c3(pa, 2), lambda: make_c5(pa),
+        for make in (lambda: make_c2_scattered(pa, args.pools), lambda: make_c2_fp32io(pa, args.pools),
+                     lambda: make_c3(pa, 2), lambda: make_c5(pa),
                      lambda: make_c2_fp8(pa, args.pools),
                      lambda: make_c3_fp8(pa, 2), lambda: make_gqa8(pa, 2)):
             w = make()
@@ -1265,6 +1296,8 @@ def main():
                     w.name, rec["kernels"].split("; ")[0], w.bytes)
             if w.name == "decode_c5":
                 rec["k_base_offset_elements"] = int(w.k_offset_elems)
+            if isinstance(w, ScatteredWorkload):
+                rec["pool_GB"] = round(w.pool_gb(), 2)
             also.append(rec)
             del w
         for name, kw in PREFILL_CFG.items():

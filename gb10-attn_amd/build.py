@@ -79,7 +79,57 @@ def build_torch_ops(verbose: bool = False) -> Path:
     return TORCH_LIB
 
 
+_REMARK_KEYS = {"TotalSGPRs": "SGPRs", "VGPRs": "VGPRs", "AGPRs": "AGPRs",
+                "ScratchSize [bytes/lane]": "scratch B/lane", "Occupancy [waves/SIMD]": "waves/SIMD",
+                "SGPRs Spill": "SGPR spills", "VGPRs Spill": "VGPR spills", "LDS Size [bytes/block]": "LDS B"}
+
+
+def resources() -> str:
+    """Per-kernel register, LDS, scratch and occupancy figures of every
+    csrc/*.hip kernel, from the compiler's kernel-resource-usage remarks
+    (same flags as build()), as a markdown table.  Occupancy is the
+    compiler's waves per SIMD from registers and LDS alone."""
+    import re
+
+    def remarks(src):
+        cmd = [HIPCC, *FLAGS, "--cuda-device-only", "-c", str(src), "-o", os.devnull,
+               "-Rpass-analysis=kernel-resource-usage"]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stderr[-6000:]}")
+        return src, r
+
+    srcs = sorted(CSRC.glob("*.hip"))
+    jobs = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
+    with ThreadPoolExecutor(jobs) as ex:
+        results = list(ex.map(remarks, srcs))
+    rows = []
+    for src, r in results:
+        cur = None
+        for line in r.stderr.splitlines():
+            m = re.search(r"remark: Function Name: (\S+)", line)
+            if m:
+                cur = {"file": src.name, "mangled": m.group(1)}
+                rows.append(cur)
+                continue
+            m = re.search(r"remark:\s+([^:]+(?:\[[^\]]*\])?): (\S+) \[-Rpass", line)
+            if m and cur is not None and m.group(1).strip() in _REMARK_KEYS:
+                cur[_REMARK_KEYS[m.group(1).strip()]] = m.group(2)
+    names = subprocess.run(["c++filt"], input="\n".join(r["mangled"] for r in rows), capture_output=True,
+                           text=True, check=True).stdout.splitlines()
+    cols = list(_REMARK_KEYS.values())
+    out = ["| kernel | file | " + " | ".join(cols) + " |", "|---|---|" + "---|" * len(cols)]
+    for r, n in zip(rows, names):
+        n = n.replace("(pa::DecodeParams)", "").replace("(pa::PrefillParams)", "").replace(
+            "(pa::ReduceParams)", "").replace("(pa::WriteParams)", "")
+        out.append(f"| `{n}` | {r['file']} | " + " | ".join(r.get(c, "") for c in cols) + " |")
+    return "\n".join(out) + "\n"
+
+
 if __name__ == "__main__":
+    if sys.argv[1:] == ["--resources"]:
+        print(resources(), end="")
+        sys.exit(0)
     build(verbose=True)
     build_torch_ops(verbose=True)
     sys.exit(0)

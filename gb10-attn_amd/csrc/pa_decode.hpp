@@ -74,6 +74,16 @@ struct DecodeShape {
   static constexpr int TT = NI * TPI;          // tokens per wave tile
 };
 
+// The shape decode_kernel<KV, D, GC, HP, *> runs: one unpacked MHA head takes
+// 2 loads per lane per tile (config 2 +0.8 % over 4).
+template <typename KV, int D, int GC, int HP>
+using DecodeShapeOf = DecodeShape<KV, D * HP, (GC == 1 && HP == 1) ? 2 : 0>;
+
+// Explicit short partitions (DecodeParams::wave_parts): one per wave, or one
+// per token slot of a wave (TPI per wave).
+constexpr int kWavePart = 1;
+constexpr int kSlotPart = 2;
+
 constexpr int kDecodeWaves = 4;
 constexpr int kDecodeThreads = 64 * kDecodeWaves;
 constexpr int kBtChunk = 256;  // block-table entries staged in LDS at a time
@@ -112,7 +122,7 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
 void decode_kernel(const DecodeParams p) {
   static_assert(DQ == 0 || (pair_types<KV>::value & (1 << DQ)), "the cache cannot provide q's pairs");
   constexpr bool LAZY = GC >= 2;  // raise the softmax reference point only by more than 2^8
-  using Sh = DecodeShape<KV, D * HP, (GC == 1 && HP == 1) ? 2 : 0>;  // one unpacked MHA head: 2 loads per lane per tile (config 2 +0.8 % over 4)
+  using Sh = DecodeShapeOf<KV, D, GC, HP>;
   constexpr int VEC = Sh::VEC, LPT = Sh::LPT, TPI = Sh::TPI, NI = Sh::NI, TT = Sh::TT;
   // Packed P.V for GQA groups over fp16 or FP8 caches (V as fp16 pairs);
   // bf16 weights would be too coarse, so bf16 caches keep the fp32 path.
@@ -157,18 +167,24 @@ void decode_kernel(const DecodeParams p) {
   int id = blockIdx.x;
   int y = id % units_y;
   id /= units_y;
-  // Wave-partition mode: work-group `grp` serves partitions grp * NW + w,
-  // one per wave w (short chunks: one partition is a few wave tiles, and a
-  // work-group per partition would pay its start-up for each).
-  const bool wpm = p.wave_parts != 0;
-  const int ngrp = (p.parts + NW - 1) / NW;
-  int part, z, grp = 0;
+  // Short explicit partitions (one is a few wave tiles, and a work-group per
+  // partition would pay its start-up for each).  Wave-partition mode:
+  // work-group `grp` serves partitions grp * NW + w, one per wave w.
+  // Slot-partition mode: it serves grp * NW * TPI + w * TPI + s, one per
+  // token slot s of wave w: a slot's lanes stream their own partition's
+  // tokens, so the wave's slot streams are the partials themselves, with no
+  // cross-slot combine per partition.
+  const bool wpm = p.wave_parts == kWavePart;
+  const bool spm = p.wave_parts == kSlotPart;
+  const int gparts = spm ? NW * TPI : wpm ? NW : 1;  // partitions per work-group
+  const int ngrp = (p.parts + gparts - 1) / gparts;
+  int part, z, grp = 0;  // part: per lane in the slot-partition mode
   if (compact_grid(p)) {
     if (!compact_unit(p, id, lane, z, part)) return;  // work-group uniform
-  } else if (wpm) {
+  } else if (wpm || spm) {
     grp = id % ngrp;
     z = id / ngrp;
-    part = grp * NW + wave;
+    part = grp * gparts + (spm ? wave * TPI + slot : wave);
   } else {
     part = id % p.parts;
     z = id / p.parts;
@@ -179,7 +195,7 @@ void decode_kernel(const DecodeParams p) {
   // every token row (12 heads on 8 XCDs); rotated, each XCD's requests cover
   // all slice offsets: config 2 6.17 -> 6.40 TB/s.  GQA and packed groups
   // measured slightly slower with it (-0.3 to -0.8 %) and keep the plain order.
-  if constexpr (GC == 1 && HP == 1) y = (y + (wpm ? z * ngrp + grp : z * p.parts + part)) % units_y;
+  if constexpr (GC == 1 && HP == 1) y = (y + (wpm || spm ? z * ngrp + grp : z * p.parts + part)) % units_y;
   const int kvh = y / p.head_chunks;  // first KV head: kvh * HP
   const int hc = y - kvh * p.head_chunks;
   const int b = z / p.Sq;
@@ -203,10 +219,10 @@ void decode_kernel(const DecodeParams p) {
   // Packed 16-bit MHA rows (config 5) measured -2.5 % with it and keep the
   // plain order, except in the wave-partition mode, whose short partitions
   // are mostly start-up.
-  const bool bt_early = !(GC == 1 && HP > 1 && KV::kCode != kFP8) || wpm;  // work-group uniform
+  const bool bt_early = !(GC == 1 && HP > 1 && KV::kCode != kFP8) || wpm || spm;  // work-group uniform
   const int64_t chunk_guess = ((int64_t)p.MB * p.BS + p.parts - 1) / p.parts;
   const int pg_early = p.part_tokens > 0 ? (int)(((int64_t)part * p.part_tokens) / p.BS)
-                                         : (int)(((wpm ? (int64_t)grp * NW : (int64_t)part) * chunk_guess) / p.BS);
+                                         : (int)(((wpm || spm ? (int64_t)grp * gparts : (int64_t)part) * chunk_guess) / p.BS);
   int32_t bt_pre = 0;
   if (bt_early && pg_early + (int)threadIdx.x < p.MB)
     bt_pre = p.block_tables[(int64_t)b * p.bt_stride + pg_early + threadIdx.x];
@@ -233,22 +249,23 @@ void decode_kernel(const DecodeParams p) {
     }
     return;
   }
-  if (wpm ? grp * NW >= nparts : part >= nparts) return;  // work-group uniform
+  if (wpm || spm ? grp * gparts >= nparts : part >= nparts) return;  // work-group uniform
 
-  // This wave's tokens [t0, t1); the work-group's [T0, T1) (wave-partition
-  // mode: its waves' partitions together; otherwise the same range).
-  int t0, t1, T0, T1;
+  // This wave's (slot-partition mode: this lane's) tokens [t0, t1); the
+  // work-group's [T0, T1) (wave- and slot-partition modes: its partitions
+  // together; otherwise the same range).
+  int t0, t1, T0, T1, chunk = 0;
   if (fixed) {
     t0 = part * p.part_tokens;
     t1 = min(t0 + p.part_tokens, ctx);
     T0 = t0;
     T1 = t1;
   } else {
-    const int chunk = (ctx + p.parts - 1) / p.parts;  // kernels/paged_attn_v3.cu:65-68
+    chunk = (ctx + p.parts - 1) / p.parts;  // kernels/paged_attn_v3.cu:65-68
     t0 = min(part * chunk, ctx);
     t1 = min(t0 + chunk, ctx);
-    T0 = wpm ? min(grp * NW * chunk, ctx) : t0;
-    T1 = wpm ? min(T0 + NW * chunk, ctx) : t1;
+    T0 = wpm || spm ? min(grp * gparts * chunk, ctx) : t0;
+    T1 = wpm || spm ? min(T0 + gparts * chunk, ctx) : t1;
   }
 
   // This lane's slice of q for the GC heads, pre-scaled into log2 units.
@@ -321,12 +338,13 @@ void decode_kernel(const DecodeParams p) {
   // LDS-staged chunk starting at page cp).  Every lane loads: a token past
   // the partition end, or on a page with an invalid block id, reads row 0 of
   // block 0 (always in bounds, NB >= 1) and is masked out of the softmax.
-  auto issue = [&](int tile, int cp, int ct1, Tile& T) {
+  // tok(i): this lane's token of load i; ct1: this lane's end.
+  auto issue_at = [&](auto&& tok, int cp, int ct1, Tile& T) {
     int blk[NI], off[NI];
     bool val[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int t = tile + i * TPI + slot;
+      const int t = tok(i);
       val[i] = t < ct1;
       const int tt = val[i] ? t : ct1 - 1;
       const int pg = (int)fastdiv((uint32_t)tt, p.bs_div);
@@ -348,6 +366,9 @@ void decode_kernel(const DecodeParams p) {
     // Keep the loads here: the scheduler would otherwise sink them next to
     // their uses (to save registers) and serialise memory behind compute.
     __builtin_amdgcn_sched_barrier(0);
+  };
+  auto issue = [&](int tile, int cp, int ct1, Tile& T) {
+    issue_at([&](int i) { return tile + i * TPI + slot; }, cp, ct1, T);
   };
 
   // Fast gather.  When BS is a multiple of TPI and tiles start on multiples
@@ -619,6 +640,78 @@ void decode_kernel(const DecodeParams p) {
     }
   };
 
+  // Rebase each stream from its lazy reference point onto its true maximum
+  // (the partials carry the maximum, kernels/paged_attn_v3.cu:113-122).
+  auto rebase = [&]() {
+    if constexpr (LAZY) {
+      if constexpr (PBC) {  // the heads' maxima and row sums live in the quad's lanes
+        mx[0] = dpp_quad<0x00>(mx_own);
+        mx[1] = dpp_quad<0x55>(mx_own);
+        mx[2] = dpp_quad<0xAA>(mx_own);
+        mx[3] = dpp_quad<0xFF>(mx_own);
+        l[0] = dpp_quad<0x00>(l_own);
+        l[1] = dpp_quad<0x55>(l_own);
+        l[2] = dpp_quad<0xAA>(l_own);
+        l[3] = dpp_quad<0xFF>(l_own);
+      }
+#pragma unroll
+      for (int g = 0; g < GC; ++g) {
+        const float corr = fast_exp2(m[g] - mx[g]);
+        l[g] *= corr;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[g][e] *= corr;
+        m[g] = mx[g];
+      }
+    }
+  };
+
+  if (spm) {
+    // The work-group's block-table entries in one staged chunk (the host
+    // enables the mode only when they fit).  Each slot streams its own
+    // partition, NI consecutive tokens per tile (a token past its end reads
+    // the masked safe row); the tile count is the chunk's, wave-uniform.
+    if (T0 < T1) {
+      const int cp = (int)fastdiv((uint32_t)T0, p.bs_div);
+      const int np = (int)fastdiv((uint32_t)(T1 - 1), p.bs_div) + 1 - cp;
+      if (bt_early && cp == pg_early) {
+        static_assert(kBtChunk <= kDecodeThreads, "one prefetched entry per thread");
+        if ((int)threadIdx.x < np) s_bt[threadIdx.x] = bt_pre;
+      } else {
+        for (int i = threadIdx.x; i < np; i += kDecodeThreads) s_bt[i] = bt_row[cp + i];
+      }
+      __syncthreads();
+      auto iss = [&](int u, Tile& T) { issue_at([&](int i) { return t0 + u + i; }, cp, t1, T); };
+      const int nt = (chunk + NI - 1) / NI;
+      Tile A, B;
+      iss(0, A);
+      for (int j = 0; j + 1 < nt; j += 2) {
+        iss((j + 1) * NI, B);
+        consume(A);
+        iss((j + 2) * NI, A);
+        consume(B);
+      }
+      if (nt & 1) consume(A);
+    }
+    rebase();
+    // This slot's partition: its partials from its lanes (dims dsub * VEC ..
+    // of head hl), m and l from those of dsub 0.
+    if (part < nparts) {
+#pragma unroll
+      for (int g = 0; g < GC; ++g) {
+        if (g0 + g >= p.G) continue;
+        const int h = (kvh * HP + hl) * p.G + g0 + g;
+        const int64_t pidx = ((int64_t)b * p.H + h) * p.parts + part;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) p.ws_acc[pidx * D + dsub * VEC + e] = acc[g][e] * p.vscale;
+        if (dsub == 0) {
+          p.ws_m[pidx] = m[g];
+          p.ws_l[pidx] = bad ? __builtin_nanf("") : l[g];
+        }
+      }
+    }
+    return;
+  }
+
   const bool fast = (p.BS % TPI) == 0 && (t0 % TPI) == 0;
   if (T0 < T1) {
     const int pg0 = (int)fastdiv((uint32_t)T0, p.bs_div);
@@ -677,28 +770,7 @@ void decode_kernel(const DecodeParams p) {
     }
   }
 
-  // Rebase each stream from its lazy reference point onto its true maximum
-  // (the partials carry the maximum, kernels/paged_attn_v3.cu:113-122).
-  if constexpr (LAZY) {
-    if constexpr (PBC) {  // the heads' maxima and row sums live in the quad's lanes
-      mx[0] = dpp_quad<0x00>(mx_own);
-      mx[1] = dpp_quad<0x55>(mx_own);
-      mx[2] = dpp_quad<0xAA>(mx_own);
-      mx[3] = dpp_quad<0xFF>(mx_own);
-      l[0] = dpp_quad<0x00>(l_own);
-      l[1] = dpp_quad<0x55>(l_own);
-      l[2] = dpp_quad<0xAA>(l_own);
-      l[3] = dpp_quad<0xFF>(l_own);
-    }
-#pragma unroll
-    for (int g = 0; g < GC; ++g) {
-      const float corr = fast_exp2(m[g] - mx[g]);
-      l[g] *= corr;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[g][e] *= corr;
-      m[g] = mx[g];
-    }
-  }
+  rebase();
 
   // Combine the TPI slot streams of this wave (log-sum-exp rule).
 #pragma unroll
@@ -819,8 +891,19 @@ hipError_t launch_decode_one(const DecodeParams& p, int64_t blocks, hipStream_t 
 }
 
 template <typename KV, int D, int GC, int HP = 1>
-hipError_t launch_decode_dg(const DecodeParams& p, hipStream_t stream) {
-  const int64_t groups = p.wave_parts ? (p.parts + kDecodeWaves - 1) / kDecodeWaves : p.parts;
+hipError_t launch_decode_dg(const DecodeParams& p0, hipStream_t stream) {
+  DecodeParams p = p0;
+  // Short explicit partitions: one per token slot when every slot of a
+  // work-group has one (parts >= kDecodeWaves * TPI) and the work-group's
+  // pages fit one staged block-table chunk; else one per wave.
+  constexpr int TPI = DecodeShapeOf<KV, D, GC, HP>::TPI;
+  if (p.wave_parts) {
+    const int64_t chunk_max = ((int64_t)p.MB * p.BS + p.parts - 1) / p.parts;
+    const int64_t pages = ((int64_t)kDecodeWaves * TPI * chunk_max + p.BS - 1) / p.BS + 1;
+    p.wave_parts = p.parts >= kDecodeWaves * TPI && pages <= kBtChunk ? kSlotPart : kWavePart;
+  }
+  const int64_t gparts = p.wave_parts == kSlotPart ? kDecodeWaves * TPI : p.wave_parts ? kDecodeWaves : 1;
+  const int64_t groups = (p.parts + gparts - 1) / gparts;
   const int64_t blocks = (int64_t)p.B * p.Sq * (p.HKV / HP) * p.head_chunks * groups;
   constexpr int PTS = pair_types<KV>::value;
   if constexpr ((PTS >> kF16) & 1) {
