@@ -63,6 +63,14 @@ __device__ inline void lds_dma16(const void* g, lds_void_t* lds) {
   __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
 }
 
+// The same load as inline asm (M0 set by the compiler from the operand).  The
+// compiler does not see it write LDS, so it places no wait for it before later
+// LDS reads; the caller waits (vmcnt) before the barrier that publishes the data.
+__device__ inline void lds_dma16_async(const void* g, lds_void_t* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(m));
+}
+
 template <bool kBf16>
 __device__ inline f32x16_t mfma32(const u32x4_t& a, const u32x4_t& b, const f32x16_t& c) {
   if constexpr (kBf16) {
@@ -766,10 +774,521 @@ void prefill_mfma_kernel(const PrefillParams p) {
   }
 }
 
+// Ping-pong prefill (64-key tiles, 16-bit caches, q in the KV type).  A
+// work-group of 8 waves serves 256 query rows (wave w owns rows 32w ..) and
+// is the only one on its CU, so each SIMD holds wave s of group 0 (waves 0-3)
+// and wave s + 4 of group 1.  Every phase ends at a work-group barrier, and
+// group 1 runs one phase behind group 0: in each phase one group does its
+// matrix step (O^T += V^T . P^T of tile j - 1, then S^T = K . Q^T of tile j)
+// while the other does its vector step (the softmax of its S^T of tile j),
+// so each SIMD issues one wave's MFMAs against the other wave's vector work.
+// In the four-wave kernel the two waves of a SIMD belong to different
+// work-groups, drift into the same step and queue behind each other.
+//
+// Phase ph, group g: step e = ph - g; even e = matrix step e / 2, odd e =
+// vector step e / 2.  Tile j's K is read in phases 2j (group 0) and 2j + 1
+// (group 1), its V (by the P.V of step j + 1) in 2j + 2 and 2j + 3.  Loads:
+//  * K of tile j + 2: group 1, direct to LDS at the end of its matrix step j
+//    (phase 2j + 1) into the third K buffer (the other waves of the group may
+//    still be reading K of tile j), waited at the end of its vector step j
+//    (phase 2j + 2);
+//  * V of tile j: group 0 at the end of its matrix step j (phase 2j), into
+//    registers (bf16, converted to fp16) or direct to LDS, finished (converted,
+//    substituted rows zeroed) and waited in its vector step (phase 2j + 1).
+// Every load is waited in a vector step, which reads no tile from LDS, so
+// the compiler's wait for direct-to-LDS loads before a tile read falls on
+// loads that are already complete.  Per-row offset tables (three, tile t in
+// t % 3) are built by wave 0 in its vector step j for tile j + 3.
+template <int N>
+struct Slot {  // a compile-time buffer index
+  static constexpr int value = N;
+};
+
+constexpr int kPpThreads = 512;  // 8 waves
+constexpr int kPpRows = 256;     // query rows per work-group
+
+template <typename KV, int D>
+__global__ __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_pp_kernel(const PrefillParams p) {
+  using Sh = PfShape<D>;
+  static_assert(Sh::KB == 64 && Sh::MT == 2, "64-key tiles");
+  constexpr int QW = 32, QB = kPpRows, KB = 64, MT = 2, KS = Sh::KS, DT = Sh::DT, NCH = Sh::NCH;
+  constexpr int CPT = Sh::CPT;  // chunks per thread of one group (256 threads) per tile
+  constexpr bool kBf16 = KV::kCode == kBF16;
+  constexpr int EB = 2;
+  static_assert(KV::kBytes == 2, "16-bit caches");
+
+  __shared__ __attribute__((aligned(16))) uint16_t sK[3][KB * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[3][KB * D];
+  __shared__ int32_t s_bt[kPfBtStage];
+  __shared__ u64x2_t s_off[3][KB];
+  __shared__ int s_badkey;
+  __shared__ int s_ovf;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;
+  const int w4 = wave & 3;
+  const int n = lane & 31;
+  const int hh = lane >> 5;
+
+  // Work-group -> unit (b, h, query block), as the four-wave kernel.
+  const int nq = p.q_tiles;
+  const int64_t nbh = (int64_t)p.B * p.H;
+  int64_t x = blockIdx.x;
+  if (p.wg_cus > 0) {
+    const int64_t C = p.wg_cus, g = x / C, jj = x - g * C;
+    if ((g & 1) && (g + 1) * C <= nbh * nq) x = g * C + (C % 8 == 0 ? C - 8 - (jj & ~(int64_t)7) + (jj & 7) : C - 1 - jj);
+  }
+  const int qt = nq - 1 - (int)(x / nbh);
+  const int64_t bh = x % nbh;
+  const int h = (int)(bh % p.H);
+  const int b = (int)(bh / p.H);
+  const int kvh = h / p.G;
+
+  int S = p.S;
+  int64_t tok0 = (int64_t)b * p.S;
+  if (p.cu_q) {
+    const int qa = p.cu_q[b], qb = p.cu_q[b + 1];
+    const bool ok = qa >= 0 && qb >= qa && (int64_t)qb <= p.q_total;
+    S = ok ? qb - qa : 0;
+    tok0 = ok ? qa : 0;
+    if (p.skip_single && S == 1) return;
+  }
+  const int Sr = min(S, p.S);
+  const int qs0 = qt * QB;
+  if (qs0 >= Sr) return;
+  const int qw0 = qs0 + wave * QW;
+  const int qrow = qw0 + n;
+  const bool live = qrow < Sr;
+
+  // Issued before the context length arrives: the block table's first
+  // min(MB, kPfBtStage) entries (the window; the host serves only tables that
+  // fit it) and this lane's q.
+  const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
+  const int nbt = min(p.MB, kPfBtStage);
+  static_assert(kPfBtStage == 2 * kPpThreads, "two entries per thread");
+  int32_t btp0 = 0, btp1 = 0;
+  if ((int)threadIdx.x < nbt) btp0 = bt_row[threadIdx.x];
+  if ((int)threadIdx.x + kPpThreads < nbt) btp1 = bt_row[threadIdx.x + kPpThreads];
+  u32x4_t qf[KS];
+  {
+    const int64_t qoff = ((tok0 + (live ? qrow : 0)) * p.H + h) * D + hh * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4_t r = u32x4_t{0u, 0u, 0u, 0u};
+      if (live) r = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p.q) + qoff + ks * 16);
+      qf[ks] = (r & p.q_and) ^ p.q_xor;
+    }
+  }
+  const int ctx = p.context_lens[b];
+  const int maxctx = p.MB * p.BS;
+
+  if (ctx > maxctx) {
+    if (live && hh == 0) {
+      const float fillv = ctx - S + qrow < 0 ? 0.0f : __builtin_nanf("");
+      const int64_t orow = ((tok0 + qrow) * p.H + h) * D;
+      for (int d = 0; d < D; ++d) store_elem(p.out, p.out_dtype, orow + d, fillv);
+    }
+    return;
+  }
+  if (threadIdx.x == 0) {
+    s_badkey = 0x7fffffff;
+    s_ovf = 0;
+  }
+
+  const int kend = min(ctx, ctx - S + min(qs0 + QB, Sr));
+  const int ntiles = kend > 0 ? (kend + KB - 1) / KB : 0;
+  const int wave_last = min(qw0 + QW - 1, Sr - 1);
+  const int wave_kend = qw0 < Sr ? min(ctx, ctx - S + wave_last + 1) : 0;
+  const int wave_kfull = ctx - S + qw0 + 1;
+  const int qpos = ctx - S + qrow;
+  const int qlim = min(qpos, kend - 1);
+
+  const float qscale = p.qscale;
+
+  // The block ids of every page the work-group reads.
+  const int npages = kend > 0 ? min((int)fastdiv((uint32_t)(kend - 1), p.bs_div) + 1, nbt) : 0;
+  if ((int)threadIdx.x < npages) s_bt[threadIdx.x] = btp0;
+  if ((int)threadIdx.x + kPpThreads < npages) s_bt[threadIdx.x + kPpThreads] = btp1;
+
+  const char* kbase = static_cast<const char*>(p.k) + (int64_t)kvh * p.k_sh * EB;
+  const char* vbase = static_cast<const char*>(p.v) + (int64_t)kvh * p.v_sh * EB;
+  const uint32_t k_sbb = (uint32_t)(p.k_sb * EB), k_stb = (uint32_t)(p.k_st * EB);
+  const uint32_t v_sbb = (uint32_t)(p.v_sb * EB), v_stb = (uint32_t)(p.v_st * EB);
+  const uint64_t nb = (uint64_t)p.num_blocks;
+
+  // This thread's chunks of a tile within its group (the four-wave kernel's
+  // mapping with w4 for the wave).
+  int prow[CPT], ksrc[CPT], vsrc[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int pos = (c * 4 + w4) * 64 + lane;
+    prow[c] = pos / NCH;
+    ksrc[c] = kpos<D>(prow[c], pos % NCH) * 8 * EB;
+    vsrc[c] = vpos<D>(prow[c], pos % NCH) * 8 * EB;
+  }
+  int badkey = 0x7fffffff;
+
+  // Wave 0: the offset table of tile t (entry r = {K byte offset, V byte
+  // offset | use}; a row past kend or on an invalid block id reads row 0 of
+  // block 0 with use = 0).
+  auto build = [&](auto slot, int t) {
+    const int row = lane;
+    const int kabs = t * KB + row;
+    const bool valid = kabs < kend;
+    const int kk = valid ? kabs : 0;
+    const int pg = (int)fastdiv((uint32_t)kk, p.bs_div);
+    const int off = kk - pg * p.BS;
+    const int blk = s_bt[valid ? pg : 0];
+    const bool okb = (uint64_t)(int64_t)blk < nb;
+    if (valid && !okb) badkey = min(badkey, kabs);
+    const bool use = valid && okb;
+    const uint32_t ub = use ? (uint32_t)blk : 0u, uo = use ? (uint32_t)off : 0u;
+    s_off[decltype(slot)::value][row] = u64x2_t{(uint64_t)ub * k_sbb + uo * k_stb,
+                                ((uint64_t)ub * v_sbb + uo * v_stb) | (use ? 1u : 0u)};
+  };
+
+  f32x16_t o[DT];
+  float m = -__builtin_inff(), l = 0.0f;
+
+  auto run = [&](auto mode_tag) -> bool {
+    constexpr int kMode = decltype(mode_tag)::value;
+    constexpr bool kDirectV = kMode != kPvConvert;
+    constexpr bool kPvBf16 = kMode == kPvSplit;
+
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] = 0.0f;
+    }
+    m = -__builtin_inff();
+    l = 0.0f;
+
+    u32x4_t vreg[kDirectV ? 1 : CPT];
+    uint32_t umask = 0;
+
+    // Group 1: K of tile t straight to LDS.
+    auto issue_k = [&](auto slot) {
+      const u64x2_t* tb = s_off[decltype(slot)::value];
+      uint16_t* dK = sK[decltype(slot)::value];
+      uint64_t e[CPT];  // the K halves of all table entries first: one LDS round trip
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) e[c] = reinterpret_cast<const uint64_t*>(tb + prow[c])[0];
+#pragma unroll
+      for (int c = 0; c < CPT; ++c)
+        lds_dma16_async(kbase + e[c] + ksrc[c], (lds_void_t*)(dK + (c * 4 + w4) * 512));
+    };
+    // Group 0: V of tile t (to LDS, or to registers for conversion).
+    auto issue_v = [&](auto slot) {
+      const u64x2_t* tb = s_off[decltype(slot)::value];
+      uint16_t* dV = sV[decltype(slot)::value];
+      umask = 0;
+      uint64_t e[CPT];  // the V halves of all table entries first: one LDS round trip
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) e[c] = reinterpret_cast<const uint64_t*>(tb + prow[c])[1];
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        const uint32_t use = (uint32_t)e[c] & 1u;
+        umask |= use << c;
+        const char* va = vbase + (e[c] - use) + vsrc[c];
+        if constexpr (kDirectV) {
+          lds_dma16_async(va, (lds_void_t*)(dV + (c * 4 + w4) * 512));
+        } else {
+          vreg[c] = *reinterpret_cast<const u32x4_t*>(va);
+        }
+      }
+    };
+    // Group 0, after its V loads are complete: zero substituted rows, or
+    // convert the staged bf16 V to fp16 (exact for 2^-17 <= |v| < 65504).
+    auto finish_v = [&](auto slot) {
+      uint16_t* dV = sV[decltype(slot)::value];
+      if constexpr (kDirectV) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads are not tracked by the compiler
+        if (umask != (1u << CPT) - 1u) {
+#pragma unroll
+          for (int c = 0; c < CPT; ++c) {
+            if (!((umask >> c) & 1u))
+              *reinterpret_cast<u32x4_t*>(dV + ((c * 4 + w4) * 64 + lane) * 8) = u32x4_t{0u, 0u, 0u, 0u};
+          }
+        }
+      } else {
+        const bool all_used = __builtin_amdgcn_ballot_w64(umask != (1u << CPT) - 1u) == 0;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+          u32x4_t w;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t xv = vreg[c][j];
+            w[j] = pack2<false>(__builtin_bit_cast(float, xv << 16), __builtin_bit_cast(float, xv & 0xffff0000u));
+          }
+          if (!all_used) {
+            asm volatile("");
+            if (!((umask >> c) & 1u)) w = u32x4_t{0u, 0u, 0u, 0u};
+          }
+          *reinterpret_cast<u32x4_t*>(dV + ((c * 4 + w4) * 64 + lane) * 8) = w;
+        }
+      }
+    };
+
+    f32x16_t st[MT];
+    u32x4_t pb[MT][2], pb_lo[kPvBf16 ? MT : 1][2];
+    // Softmax of tile t: mask, lazy maximum, P^T operands (see the four-wave kernel).
+    auto softmax = [&](int t) {
+      const int tk0 = t * KB;
+      if (tk0 + KB > wave_kfull) {
+        asm volatile("");
+        const int thr = qlim - tk0 - 4 * hh;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            if (mt * 32 + 8 * (r >> 2) + (r & 3) > thr) st[mt][r] = -__builtin_inff();
+          }
+        }
+      }
+      // Maximum over four independent chains (short dependency chains).
+      float mc[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        mc[c] = st[c >> 1][(c & 1) * 8];
+#pragma unroll
+        for (int r = 1; r < 8; ++r) mc[c] = fmaxf(mc[c], st[c >> 1][(c & 1) * 8 + r]);
+      }
+      const float mx = fmaxf(fmaxf(mc[0], mc[1]), fmaxf(mc[2], mc[3]));
+      const float mxh = mx * qscale;
+      if (__builtin_amdgcn_ballot_w64(mxh > m + kLazyRescale) != 0) {
+        asm volatile("");
+        const float mxs = fmaxf(mxh, __shfl_xor(mxh, 32, 64));
+        const float mn = fmaxf(m, mxs);
+        const float corr = mn == -__builtin_inff() ? 1.0f : fast_exp2(m - mn);
+        m = mn;
+        l *= corr;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;
+      }
+      const float negm = m == -__builtin_inff() ? 0.0f : -m;
+      // The row sum over the rounded weights in four chains, added at the end.
+      float ls[MT][2];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          uint32_t w[4], wl[4];
+          float lc = 0.0f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float p0 = fast_exp2(fmaf(st[mt][8 * s2 + 2 * j], qscale, negm));
+            const float p1 = fast_exp2(fmaf(st[mt][8 * s2 + 2 * j + 1], qscale, negm));
+            w[j] = pack2<kPvBf16>(p0, p1);
+            if constexpr (kPvBf16) {
+              const float2_t r = unpack2<true>(w[j]);
+              wl[j] = pack2<true>(p0 - r[0], p1 - r[1]);
+              lc += p0 + p1;
+            } else {
+              lc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w[j]), half2_t{1.0f16, 1.0f16}, lc, false);
+            }
+          }
+          ls[mt][s2] = lc;
+          pb[mt][s2] = u32x4_t{w[0], w[1], w[2], w[3]};
+          if constexpr (kPvBf16) pb_lo[mt][s2] = u32x4_t{wl[0], wl[1], wl[2], wl[3]};
+        }
+      }
+      l += (ls[0][0] + ls[0][1]) + (ls[1][0] + ls[1][1]);
+    };
+    // Matrix step: O^T += V^T . P^T of tile j - 1 (V in slot SV), then
+    // S^T = K . Q^T of tile j (K in slot SK).  Each LDS operand is read two
+    // MFMAs ahead into a ring of three, in this order (fences keep the
+    // scheduler from regrouping the reads next to their uses), and the first
+    // two K operands are read before the P.V products.
+    const int li = lane & 15;
+    const int trow = 4 * hh + (li >> 2);
+    const int tcol = 16 * ((lane >> 4) & 1) + (li & 3) * 4;
+    auto mstep = [&](auto sk, auto sv, bool do_pv, bool do_qk) {
+      const uint16_t* cK = sK[decltype(sk)::value];
+      const uint16_t* cV = sV[decltype(sv)::value];
+      u32x4_t ka[3][MT];
+      auto rdk = [&](int ks, u32x4_t (&dst)[MT]) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          dst[mt] = *reinterpret_cast<const u32x4_t*>(cK + swk<D>(mt * 32 + n, 2 * ks + hh));
+      };
+      if (do_qk) {
+        rdk(0, ka[0]);
+        rdk(1, ka[1]);
+      }
+      if (do_pv) {
+        // Product i: m-tile mt = i / (2 DT), step s2 = (i / DT) % 2, dims dt = i % DT.
+        constexpr int NP = MT * 2 * DT;
+        u32x4_t va[3];
+        auto rdv = [&](int i, u32x4_t& dst) {
+          const int mt = i / (2 * DT), s2 = (i / DT) % 2, dt = i % DT;
+          const int r0 = mt * 32 + 16 * s2 + trow;
+          const int col = dt * 32 + tcol;
+          const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_short4_t*)(cV + swv<D>(r0, col >> 3) + (col & 7)));
+          const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_short4_t*)(cV + swv<D>(r0 + 8, col >> 3) + (col & 7)));
+          const uint64_t lo64 = __builtin_bit_cast(uint64_t, lo), hi64 = __builtin_bit_cast(uint64_t, hi);
+          dst = u32x4_t{(uint32_t)lo64, (uint32_t)(lo64 >> 32), (uint32_t)hi64, (uint32_t)(hi64 >> 32)};
+        };
+        rdv(0, va[0]);
+        rdv(1, va[1]);
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+          if (i + 2 < NP) rdv(i + 2, va[(i + 2) % 3]);
+          __builtin_amdgcn_sched_barrier(0);
+          const int mt = i / (2 * DT), s2 = (i / DT) % 2, dt = i % DT;
+          o[dt] = mfma32<kPvBf16>(va[i % 3], pb[mt][s2], o[dt]);
+          if constexpr (kPvBf16) o[dt] = mfma32<true>(va[i % 3], pb_lo[mt][s2], o[dt]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      if (do_qk) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) st[mt][r] = 0.0f;
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          if (ks + 2 < KS) rdk(ks + 2, ka[(ks + 2) % 3]);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) st[mt] = mfma32<kBf16>(ka[ks % 3][mt], qf[ks], st[mt]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    };
+
+    // Prologue: tables 0-2, K of tiles 0 and 1, V of tile 0.
+    __syncthreads();
+    if (wave == 0) {
+      if (ntiles > 0) build(Slot<0>{}, 0);
+      if (ntiles > 1) build(Slot<1>{}, 1);
+      if (ntiles > 2) build(Slot<2>{}, 2);
+    }
+    __syncthreads();
+    if (grp == 1) {
+      if (ntiles > 0) issue_k(Slot<0>{});
+      if (ntiles > 1) issue_k(Slot<1>{});
+    } else if (ntiles > 0) {
+      issue_v(Slot<0>{});
+      finish_v(Slot<0>{});
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+
+    // Step j (buffer slot j % 3, a compile-time index: every LDS address is a
+    // loop-invariant lane offset plus an immediate).  Every wave runs the
+    // same steps; group 1 passes one barrier first, so its k-th barrier of
+    // the loop meets group 0's (k + 1)-th: one phase behind.  Loads for a
+    // later tile start at the top of a vector step and are finished at the
+    // end of the next matrix step, two phases later.
+    auto step = [&](auto slot, int j) {
+      constexpr int B0 = decltype(slot)::value;  // tile j
+      constexpr int B1 = (B0 + 1) % 3;           // tile j + 1
+      constexpr int B2 = (B0 + 2) % 3;           // tiles j + 2 and j - 1
+      // Matrix step j.
+      mstep(Slot<B0>{}, Slot<B2>{}, j >= 1 && (j - 1) * KB < wave_kend, j < ntiles && j * KB < wave_kend);
+      __builtin_amdgcn_sched_barrier(0);
+      if (grp == 0) {
+        if (j >= 1 && j < ntiles) finish_v(Slot<B0>{});  // V of tile j, loaded since vector step j - 1
+      } else if (j + 1 < ntiles) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // K of tile j + 1, loaded since vector step j - 1
+      }
+      __syncthreads();
+      // Vector step j.
+      if (grp == 0) {
+        if (j + 1 < ntiles) issue_v(Slot<B1>{});
+      } else if (j + 2 < ntiles) {
+        issue_k(Slot<B2>{});
+      }
+      if (j < ntiles && j * KB < wave_kend) softmax(j);
+      if (wave == 0 && j + 3 < ntiles) build(Slot<B0>{}, j + 3);
+      __syncthreads();
+    };
+    if (grp == 1) __syncthreads();
+    for (int j = 0; j <= ntiles; j += 3) {  // work-group uniform exits
+      step(Slot<0>{}, j);
+      if (j + 1 > ntiles) break;
+      step(Slot<1>{}, j + 1);
+      if (j + 2 > ntiles) break;
+      step(Slot<2>{}, j + 2);
+    }
+    if (grp == 0) __syncthreads();
+    if constexpr (kMode == kPvConvert) {
+      bool bad = false;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bad |= !__builtin_isfinite(o[dt][r]);
+      }
+      if (bad) s_ovf = 1;
+      __syncthreads();
+      if (s_ovf) return false;
+    }
+    return true;
+  };
+
+  if constexpr (kBf16) {
+    if (!run(PvTag<kPvConvert>{})) {
+      badkey = 0x7fffffff;
+      run(PvTag<kPvSplit>{});
+    }
+  } else {
+    run(PvTag<kPvDirect>{});
+  }
+
+  if (badkey != 0x7fffffff) atomicMin(&s_badkey, badkey);
+  __syncthreads();
+  const int bad_from = s_badkey;
+
+  const float lt = l + __shfl_xor(l, 32, 64);
+  if (!live) return;
+  const bool bad = bad_from <= qpos;
+  const float inv = lt > 0.0f ? p.vscale / lt : 0.0f;
+  const int64_t orow = ((tok0 + qrow) * p.H + h) * D;
+  const uintptr_t oa = reinterpret_cast<uintptr_t>(p.out);
+  const bool vec = (p.out_dtype == kF32 ? (oa & 15) == 0 : (oa & 7) == 0);
+  if (!vec) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = dt * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+        store_elem(p.out, p.out_dtype, orow + d, bad ? __builtin_nanf("") : o[dt][r] * inv);
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = bad ? __builtin_nanf("") : o[dt][4 * j + i] * inv;
+      const int64_t e = orow + dt * 32 + 8 * j + 4 * hh;
+      if (p.out_dtype == kF32) {
+        u64x2_t w = u64x2_t{(uint64_t)__builtin_bit_cast(uint32_t, v[0]) | ((uint64_t)__builtin_bit_cast(uint32_t, v[1]) << 32),
+                            (uint64_t)__builtin_bit_cast(uint32_t, v[2]) | ((uint64_t)__builtin_bit_cast(uint32_t, v[3]) << 32)};
+        *reinterpret_cast<u64x2_t*>(static_cast<float*>(p.out) + e) = w;
+      } else {
+        const uint32_t w0 = p.out_dtype == kF16 ? pack2<false>(v[0], v[1]) : pack2<true>(v[0], v[1]);
+        const uint32_t w1 = p.out_dtype == kF16 ? pack2<false>(v[2], v[3]) : pack2<true>(v[2], v[3]);
+        const uint64_t w = (uint64_t)w0 | ((uint64_t)w1 << 32);
+        *reinterpret_cast<uint64_t*>(static_cast<uint16_t*>(p.out) + e) = w;
+      }
+    }
+  }
+}
+
 // CU count of the current device and resident work-groups per CU of one
 // kernel instance, cached per device; {0, 0} if unknown.
 template <typename F>
-static void residency(F kernel, std::atomic<int64_t> (&cache)[64], int64_t* cus, int64_t* per_cu) {
+static void residency(F kernel, std::atomic<int64_t> (&cache)[64], int64_t* cus, int64_t* per_cu,
+                      int threads = kPfThreads) {
   *cus = *per_cu = 0;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) return;
@@ -783,7 +1302,7 @@ static void residency(F kernel, std::atomic<int64_t> (&cache)[64], int64_t* cus,
   }
   int n = 0, k = 0;
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, kernel, kPfThreads, 0) != hipSuccess || k <= 0 ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, kernel, threads, 0) != hipSuccess || k <= 0 ||
       k > 0xff)
     return;
   if (dev < 64) cache[dev].store(((int64_t)n << 8) | k, std::memory_order_relaxed);
@@ -808,6 +1327,21 @@ static hipError_t launch_pf_q(const PrefillParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <typename KV, int D>
+static hipError_t launch_pp(const PrefillParams& p, hipStream_t stream) {
+  static std::atomic<int64_t> cache[64];
+  const auto kernel = prefill_pp_kernel<KV, D>;
+  PrefillParams q = p;
+  q.q_tiles = (p.S + kPpRows - 1) / kPpRows;
+  const int64_t units = (int64_t)q.B * q.H * q.q_tiles;
+  int64_t cus = 0, per_cu = 0;
+  residency(kernel, cache, &cus, &per_cu, kPpThreads);
+  q.wg_cus = units > cus && units <= cus * per_cu ? (int32_t)cus : 0;  // one resident wave
+  note_launch("pa::prefill_pp_kernel<%s, %d>", KV::kName, D);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)units), dim3(kPpThreads), 0, stream, q);
+  return hipGetLastError();
+}
+
 // Key-split mode when the plain grid (blocks of 128 query rows) has fewer
 // work-groups than CUs: chunks of a long context
 // (the reference's 512-token chunk at context 2048: 192 work-groups, +19 %).
@@ -822,6 +1356,13 @@ static hipError_t launch_pf(const PrefillParams& p, hipStream_t stream) {
     const int64_t plain = (int64_t)p.B * p.H * ((p.S + PfShape<D>::QB - 1) / PfShape<D>::QB);
     if (cus > 0 && plain < cus)
       return p.q_split ? launch_pf_q<KV, D, true, true>(p, stream) : launch_pf_q<KV, D, false, true>(p, stream);
+    // The 8-wave kernel (one work-group per CU) for grids of at least two
+    // of its work-groups per CU; below that its 256-row blocks leave CUs
+    // idle at the end of the launch (config 4a: 384 work-groups, -20 %).
+    if constexpr (KV::kCode == kF16 || KV::kCode == kBF16) {
+      const int64_t pp_units = (int64_t)p.B * p.H * ((p.S + kPpRows - 1) / kPpRows);
+      if (!p.q_split && p.MB <= kPfBtStage && cus > 0 && pp_units >= 2 * cus) return launch_pp<KV, D>(p, stream);
+    }
   }
   return p.q_split ? launch_pf_q<KV, D, true, false>(p, stream) : launch_pf_q<KV, D, false, false>(p, stream);
 }

@@ -323,6 +323,52 @@ def test_mfma_prefill_plain_and_key_split_modes(pa, dev, kv, qt, D):
         close(to_host(got), want_of(inp, 1.0 / np.sqrt(D)))
 
 
+def _want_head_groups(inp, scale, groups, bt=None):
+    """The oracle for the query heads of the given KV-head groups only (a
+    KV head's G query heads are contiguous), as [B, S, len(groups) * G, D]."""
+    H, HKV = inp["q_f32"].shape[2], inp["k"].shape[2]
+    G = H // HKV
+    parts = [oracle.prefill(inp["q_f32"][:, :, g * G:(g + 1) * G], inp["k"][:, :, g:g + 1], inp["v"][:, :, g:g + 1],
+                            inp["bt"] if bt is None else bt, inp["ctx"], scale, inp["kv"]) for g in groups]
+    return np.concatenate(parts, axis=2)
+
+
+@pytest.mark.parametrize("kv", ["f16", "bf16"])
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_mfma_prefill_pingpong(pa, dev, kv, D):
+    """Grids of at least two work-groups per CU with q in the KV type run the
+    8-wave kernel (256 query rows per work-group).  Chunked (S < ctx), plain
+    and padded (S > ctx) rows over GQA-4 heads, checked on the first and last
+    KV heads' query heads; then the same inputs with a page of invalid block
+    id (exactly the rows that attend it are NaN) and, for bf16, V values fp16
+    cannot hold on a few keys (the work-group reruns with V in bf16)."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    H = 4 * (-(-cus // 16))  # 4 sequences x 2 blocks of 256 rows x H heads >= 2 x CUs
+    S, BS = 260, 16
+    inp = prefill_case(4, S, H, H // 4, D, BS, [600, 120, 260, 400], seed=D + 40, kv=kv, qt=kv)
+    scale = 1.0 / np.sqrt(D)
+    groups = [0, H // 4 - 1]
+    heads = np.r_[0:4, H - 4:H]
+    print(f"pingpong kv={kv} D={D} H={H}", flush=True)
+    got = pa.paged_attention_prefill_wmma(*dev_args(inp, dev), scale)
+    assert pa.last_launch().startswith("pa::prefill_pp_kernel<"), pa.last_launch()
+    close(to_host(got)[:, :, heads], _want_head_groups(inp, scale, groups))
+
+    bt = inp["bt"].copy()
+    bt[0, 30] = 10 ** 6  # keys 480..495 of sequence 0: rows at positions >= 480 are NaN
+    if kv == "bf16":
+        v = inp["v"].copy()
+        for b, key, val in ((0, 100, 1.0e6), (0, 550, -7.0e4), (3, 50, 3.0e5)):
+            v[inp["bt"][b, key // BS], key % BS] = oracle.quantize(np.full(v.shape[2:], val, np.float32), "bf16")
+        inp["v"] = v
+    q, k, vd, _, ctx = dev_args(inp, dev)
+    got = to_host(pa.paged_attention_prefill_wmma(q, k, vd, torch.from_numpy(bt).to(dev), ctx, scale))[:, :, heads]
+    want = _want_head_groups(inp, scale, groups, bt)
+    assert np.isnan(want[0]).any() and not np.isnan(want[1:]).any()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    close(got, want)
+
+
 def fp8_prefill_case(B, S, H, HKV, D, BS, ctx, *, seed, qt, k_scale, v_scale, poison=False):
     """FP8 E4M3 pool holding K / k_scale and V / v_scale, plus the oracle's
     inputs: the dequantised values (code * scale) as fp32.  poison: NaN codes
