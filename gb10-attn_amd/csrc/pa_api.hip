@@ -165,10 +165,8 @@ int scratch_address(void** ptr) {
 // Tuning constants of the partition planner: target resident work-groups
 // per CU; the shortest partition worth a work-group (and the same for tiny
 // grids, whose time is latency, not bandwidth) and the longest (bounds ragged
-// imbalance), in tokens; the longest when the plan splits anyway and the VALU
-// kernel serves the group (finer balance for ragged batches, config 3: +4 %;
-// the matrix-core kernel, groups of 8+, amortises its set-up over the longer
-// one).
+// imbalance), in tokens.  Config 3 (ragged GQA-4, contexts to 32768) measured
+// 1024-token partitions 2.6 % slower than 2048, 3072 3.5 % slower, 4096 17 %.
 // Longest explicit partition (tokens, at the block table's capacity) served
 // in the wave-partition mode.
 constexpr int64_t kWavePartTokens = 256;
@@ -178,7 +176,6 @@ struct PlanKnobs {
   int64_t min_part = 256;
   int64_t min_part_tiny = 64;
   int64_t max_part = 2048;
-  int64_t max_part_split = 1024;
 };
 
 const PlanKnobs& knobs() {
@@ -567,8 +564,7 @@ int pa_plan_partitions(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads
   const int64_t units = std::max<int64_t>(1, num_seqs * num_kv_heads * ((G + gc - 1) / gc));
   const int64_t target = num_compute_units * kn.wgs_per_cu;
   int64_t S = (target + units - 1) / units;                             // fill the GPU
-  const int64_t max_part = S > 1 && gc < 8 ? kn.max_part_split : kn.max_part;
-  S = std::max(S, (max_context + max_part - 1) / max_part);             // bound partition length
+  S = std::max(S, (max_context + kn.max_part - 1) / kn.max_part);       // bound partition length
   // Tiny grids (the units with partitions of min_part tokens still cannot
   // fill the GPU: a few short sequences) take shorter partitions, so that
   // more work-groups have their loads in flight at once.

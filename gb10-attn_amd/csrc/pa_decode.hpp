@@ -46,21 +46,44 @@ __device__ inline bool compact_grid(const DecodeParams& p) {
   return p.part_tokens > 0 && p.Sq == 1 && p.B <= 64 && p.cu_q == nullptr;
 }
 // Unit `id` of the compacted numbering -> (z, part); false past the last one.
+// Whole partitions come first, sequence by sequence (a context out of range
+// is one unit: it writes its row), then each sequence's shorter last
+// partition, longest first: the dispatcher hands out work-groups in id
+// order, so the launch ends on its shortest units.  Config 3 (1044 units on
+// 512 slots, partitions of 13 to 2048 tokens) had ended with half the slots
+// idle for its last ~15 %.
 __device__ inline bool compact_unit(const DecodeParams& p, int id, int lane, int& z, int& part) {
   const int maxctx = p.MB * p.BS;
   const int c = lane < p.B ? p.context_lens[lane] : 0;
-  const int np = lane < p.B ? (c > 0 && c <= maxctx ? (c - 1) / p.part_tokens + 1 : 1) : 0;
-  int incl = np;  // inclusive prefix sum of the units over sequences 0..lane
+  const bool valid = lane < p.B && c > 0 && c <= maxctx;
+  const int whole = valid ? c / p.part_tokens : 0;
+  const int nfull = lane < p.B ? (valid ? whole : 1) : 0;   // units of whole partitions
+  const int rem = valid ? c - whole * p.part_tokens : 0;     // tokens of the last partition if shorter (0: none)
+  int incl = nfull;  // inclusive prefix sum over sequences 0..lane
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
     const int t = __shfl_up(incl, o, 64);
     incl += lane >= o ? t : 0;
   }
-  // Sequences whose units all precede id form a prefix of the lanes.
-  const int zz = __builtin_popcountll(__builtin_amdgcn_ballot_w64(incl <= id));
-  if (zz >= p.B) return false;
-  z = zz;
-  part = id - __builtin_amdgcn_readlane(incl - np, zz);
+  const int total_full = __builtin_amdgcn_readlane(incl, 63);
+  if (id < total_full) {
+    // Sequences whose whole partitions all precede id form a prefix of the lanes.
+    const int zz = __builtin_popcountll(__builtin_amdgcn_ballot_w64(incl <= id));
+    z = zz;
+    part = id - __builtin_amdgcn_readlane(incl - nfull, zz);
+    return true;
+  }
+  // The k-th shorter partition by length (descending; ties by sequence).
+  const int k = id - total_full;
+  int rank = 0;
+  for (int j = 0; j < 64; ++j) {
+    const int rj = __builtin_amdgcn_readlane(rem, j);
+    rank += (rj > rem || (rj == rem && j < lane)) ? 1 : 0;
+  }
+  const uint64_t hit = __builtin_amdgcn_ballot_w64(rem > 0 && rank == k);
+  if (hit == 0) return false;
+  z = __builtin_ctzll(hit);
+  part = __builtin_amdgcn_readlane(nfull, z);
   return true;
 }
 

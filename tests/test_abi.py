@@ -178,9 +178,8 @@ def test_plan_partitions(pa):
     # config 3: 32 x 8 units, contexts up to 32768 -> split, partitions bounded.
     ptok, n = pa.plan_partitions(32, 32, 8, 128, 32768, 256)
     assert n > 1 and ptok * n >= 32768 and ptok % 128 == 0 and ptok <= 2048
-    # ... and since the plan splits anyway and groups of 4 run on the VALU kernel, 1024-token partitions;
-    # groups of 8 (matrix-core kernel) keep 2048-token partitions.
-    assert (ptok, n) == (1024, 32)
+    # ... at the longest partition, 2048 tokens (groups of 4 and of 8 alike).
+    assert (ptok, n) == (2048, 16)
     assert pa.plan_partitions(32, 64, 8, 128, 8192, 256) == (2048, 4)
     # tiny problem: no split
     assert pa.plan_partitions(1, 1, 1, 64, 100, 256) == (100, 1)
