@@ -1161,7 +1161,7 @@ def summarize(line):
                          {k: legs.get(k, {}).get("GBs") for k in ("v1", "v2", "gather_dense_torch",
                                                                   "gather_sdpa_torch")}]
         elif "value" in r and "unit" in r:
-            frac = r.get("frac_of_8TBs", r.get("frac_of_mfma_peak"))
+            frac = r.get("frac_of_8TBs", r.get("frac_of_hbm_peak", r.get("frac_of_mfma_peak")))
             out[name] = [r["value"], r["unit"], frac, r.get("ms_per_step")]
     return out
 
