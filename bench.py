@@ -1072,20 +1072,30 @@ def sweep_records(pa, steps):
 
 
 def c2_split_records(pa, pools, steps):
-    """Config 2 through the explicit split + LSE reduce: the reference's own
-    count (choose_num_splits on its 48-SM GB10: 64) and the fastest of a few
-    explicit counts, with the partition kernel and the reduce timed apart."""
+    """Config 2 through an explicit split: the reference's own count
+    (choose_num_splits on its 48-SM GB10: 64) and the fastest of a few
+    explicit counts, each timed as the API call the reference makes
+    (paged_attention_v3 with num_splits: partition + reduce, or the fused
+    one-launch form where the plan allows it).  The reference's count is
+    also timed as two launches (pa_v3_partition, then pa_v3_reduce) with the
+    partition kernel and the reduce timed apart."""
     recs = []
     for ns in (64, 2, 4, 8, 16):
         w = DecodeWorkload(pa, B=64, H=12, HKV=12, D=64, BS=16, ctx=[2048] * 64, dtype=torch.float16,
                            pools=pools, seed=2, name=f"decode_c2_split{ns}", num_splits=ns)
         log(f"bench: {w.name}")
+        w.split = False  # one call, as the reference's v3 entry point
         ms, kms, rec = decode_record(w, max(20, steps), 5)
         if ms is not None:
             rec["num_splits"] = ns
-            rec["partition_kernel_ms"] = rec.pop("kernel_ms")
-            rec["reduce_ms"] = round(w.reduce_ms, 5)
-            rec["partition_kernel_GBs"] = round(w.bytes / (kms * 1e-3) / 1e9, 1)
+            rec["fused"] = "reduce_kernel" not in rec["kernels"]
+            if ns == 64:
+                w.split = True
+                ms2, kms2, rec2 = decode_record(w, max(20, steps), 5)
+                if ms2 is not None:
+                    rec["two_launch"] = {"value": rec2["value"], "unit": "GB/s", "ms_per_step": rec2["ms_per_step"],
+                                         "partition_kernel_ms": round(kms2, 5), "reduce_ms": round(w.reduce_ms, 5),
+                                         "partition_kernel_GBs": round(w.bytes / (kms2 * 1e-3) / 1e9, 1)}
         recs.append(rec)
         del w
     ok = [r for r in recs[1:] if r.get("value")]

@@ -45,6 +45,8 @@ hipError_t launch_decode_f32(const DecodeParams& p, int gc, hipStream_t stream);
 hipError_t launch_decode_f64(const DecodeParams& p, int gc, hipStream_t stream);
 hipError_t launch_decode_fp8(const DecodeParams& p, int gc, hipStream_t stream);
 
+thread_local int t_decode_fused = 0;
+
 hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int gc, hipStream_t stream) {
   switch (kv_dtype) {
     case kF16: return launch_decode_f16(p, gc, stream);
@@ -440,24 +442,43 @@ int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const p
   a.p.parts = (int)plan.parts;
   a.p.part_tokens = (int)plan.part_tokens;
   a.p.direct = plan.direct ? 1 : 0;
+  // Explicit splits into short chunks (the reference's own count at long
+  // contexts: 64 splits of 32 tokens at ctx 2048) run with a partition per
+  // wave or per token slot, each written as its own partials.  A call that
+  // wants the output too, over groups of one query head per KV head chunk,
+  // fuses when decode_fuse_rounds() allows it and one work-group per (row,
+  // head) at the narrowest packing still fills the GPU: that work-group
+  // serves every partition of its unit in rounds, writes their partials,
+  // merges them into the output, and the reduce launch is skipped (config 2
+  // at 64 splits: partition kernel + reduce 79.0 us per call, fused with one
+  // head per work-group 74.2 us).
+  const int64_t maxctx = (int64_t)a.p.MB * a.p.BS;
+  a.p.wave_parts = num_splits > 0 && !plan.direct && (maxctx + plan.parts - 1) / plan.parts <= kWavePartTokens;
   a.p.hp = plan.hp;
+  a.p.fuse_final = 0;
+  if (a.p.wave_parts && phases == kBoth && a.gc == 1) {
+    int cus = 0;
+    if ((rc = device_cu_count(&cus))) return rc;
+    const int kvb = dtype_bytes(a.kv_dtype);
+    const int hp = pack_for(a.p, kvb, 1, cus);
+    if ((int64_t)a.p.B * a.p.Sq * (a.p.HKV / hp) * a.p.head_chunks >= cus &&
+        decode_fuse_rounds(plan.parts, a.p.MB, a.p.BS, decode_tpi(a.p.D, hp, kvb)) > 0) {
+      a.p.fuse_final = 1;
+      a.p.hp = hp;
+    }
+  }
   if (a.p.hp == 0) {
     int cus = 0;
     if ((rc = device_cu_count(&cus))) return rc;
     a.p.hp = pack_for(a.p, dtype_bytes(a.kv_dtype), plan.parts, cus);
   }
-  // Explicit splits into short chunks (the reference's own count at long
-  // contexts: 64 splits of 32 tokens at ctx 2048) run in the wave-partition
-  // mode: one work-group per kDecodeWaves consecutive partitions, one per wave,
-  // each written as its own partials.
-  const int64_t maxctx = (int64_t)a.p.MB * a.p.BS;
-  a.p.wave_parts = num_splits > 0 && !plan.direct && (maxctx + plan.parts - 1) / plan.parts <= kWavePartTokens;
   if (!plan.direct) bind_workspace(&a.p, ws, plan);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  t_decode_fused = 0;
   if (phases & kPartition) {
     if ((rc = hip_status(launch_decode(a.p, a.kv_dtype, a.gc, s), "partition kernel launch"))) return rc;
   }
-  if ((phases & kReduce) && !plan.direct) {
+  if ((phases & kReduce) && !plan.direct && !t_decode_fused) {
     ReduceParams r;
     r.out = a.p.out;
     r.ws_acc = a.p.ws_acc;

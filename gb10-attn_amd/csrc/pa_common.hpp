@@ -61,8 +61,11 @@ struct DecodeParams {
   int32_t direct;       // 1: one partition, every WG writes the normalised output
   int32_t hp;           // KV heads per work-group (head packing: MHA, or GQA groups of four); <= 1: one
   int32_t pprio;        // 1: the whole grid is resident at once; waves lower their priority as they progress
-  int32_t wave_parts;   // 1: each wave serves a partition of its own; a work-group covers kDecodeWaves
-                        // consecutive partitions (explicit splits into short chunks)
+  int32_t wave_parts;   // explicit splits into short chunks: 1 from the host (the launcher picks the
+                        // mode: a partition per wave or per token slot); 0 otherwise
+  int32_t rounds;       // slot-partition mode: partitions each token slot serves in turn
+  int32_t fuse_final;   // host: the call wants the output too and decode_fuse_rounds() allows it;
+                        // kernel: the work-group covers every partition of its unit and writes it
   FastDiv bs_div;
   float qscale;         // scale * k_scale * log2(e): scores come out in log2 units
   float vscale;         // v_scale (FP8 caches): applied to the weighted V sum
@@ -134,12 +137,48 @@ struct WriteParams {
   int32_t t_base;              // first token of this launch (large writes take several)
 };
 
+constexpr int kDecodeWaves = 4;
+constexpr int kDecodeThreads = 64 * kDecodeWaves;
+constexpr int kBtChunk = 256;  // block-table entries a decode work-group stages in LDS at a time
+
+// Explicit short partitions (DecodeParams::wave_parts): one per wave, or one
+// per token slot of a wave (TPI per wave).
+constexpr int kWavePart = 1;
+constexpr int kSlotPart = 2;
+constexpr int kMaxSlotRounds = 8;  // most partitions per token slot in the fused mode
+
+// Token rows one decode load instruction covers (TPI: 64 lanes over rows of
+// HP * D elements, 16 bytes per lane, FP8 8), as the kernels are built.
+inline int decode_tpi(int D, int HP, int kv_bytes) {
+  const int vec = kv_bytes == 1 ? 8 : 16 / kv_bytes;
+  const int lpt = D * HP / vec;
+  return lpt >= 64 ? 1 : 64 / lpt;
+}
+
+// Fused explicit split: one work-group per (sequence, head group) serves all
+// `parts` partitions in rounds of kDecodeWaves * tpi (a partition per token
+// slot), writes each one's partials and merges them into the output itself,
+// with no reduce launch.  The rounds it takes, or 0 when there are fewer
+// partitions than slots, more rounds than kMaxSlotRounds, or the
+// work-group's pages would not fit one staged block-table chunk.
+inline int decode_fuse_rounds(int64_t parts, int MB, int BS, int tpi) {
+  const int64_t gp1 = (int64_t)kDecodeWaves * tpi;
+  if (parts < gp1 || MB <= 0 || BS <= 0) return 0;
+  const int64_t R = (parts + gp1 - 1) / gp1;
+  const int64_t chunk_max = ((int64_t)MB * BS + parts - 1) / parts;
+  const int64_t pages = (R * gp1 * chunk_max + BS - 1) / BS + 1;
+  return R <= kMaxSlotRounds && pages <= kBtChunk ? (int)R : 0;
+}
+
 // Records the kernel instance a launcher is about to dispatch, as profilers
 // print its demangled name, for pa_last_launch() (host side, per thread).
 void note_launch(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 
 // Host launchers (defined in the kernel translation units).
 hipError_t launch_decode(const DecodeParams& p, int kv_dtype, int gc, hipStream_t stream);
+// Set by the decode launcher when a launch wrote the output itself although
+// the plan splits (fuse_final took effect): no reduce launch is needed.
+extern thread_local int t_decode_fused;
 hipError_t launch_reduce(const ReduceParams& p, hipStream_t stream);
 hipError_t launch_prefill_mfma(const PrefillParams& p, int kv_dtype, hipStream_t stream);
 hipError_t launch_write_kv(const WriteParams& p, hipStream_t stream);

@@ -102,15 +102,6 @@ struct DecodeShape {
 template <typename KV, int D, int GC, int HP>
 using DecodeShapeOf = DecodeShape<KV, D * HP, (GC == 1 && HP == 1) ? 2 : 0>;
 
-// Explicit short partitions (DecodeParams::wave_parts): one per wave, or one
-// per token slot of a wave (TPI per wave).
-constexpr int kWavePart = 1;
-constexpr int kSlotPart = 2;
-
-constexpr int kDecodeWaves = 4;
-constexpr int kDecodeThreads = 64 * kDecodeWaves;
-constexpr int kBtChunk = 256;  // block-table entries staged in LDS at a time
-
 // HP > 1 (MHA, or GQA groups of four): one work-group serves HP adjacent KV
 // heads, whose rows of a token are contiguous in the pool, as one row of
 // HP * D elements (up to 512 bytes); with GC > 1 the lanes of each head's
@@ -193,13 +184,14 @@ void decode_kernel(const DecodeParams p) {
   // Short explicit partitions (one is a few wave tiles, and a work-group per
   // partition would pay its start-up for each).  Wave-partition mode:
   // work-group `grp` serves partitions grp * NW + w, one per wave w.
-  // Slot-partition mode: it serves grp * NW * TPI + w * TPI + s, one per
-  // token slot s of wave w: a slot's lanes stream their own partition's
-  // tokens, so the wave's slot streams are the partials themselves, with no
-  // cross-slot combine per partition.
+  // Slot-partition mode: it serves `rounds` rounds of NW * TPI partitions,
+  // round r's grp * gparts + r * NW * TPI + w * TPI + s for token slot s of
+  // wave w: a slot's lanes stream their own partition's tokens, so the
+  // wave's slot streams are the partials themselves, with no cross-slot
+  // combine per partition.
   const bool wpm = p.wave_parts == kWavePart;
   const bool spm = p.wave_parts == kSlotPart;
-  const int gparts = spm ? NW * TPI : wpm ? NW : 1;  // partitions per work-group
+  const int gparts = spm ? NW * TPI * p.rounds : wpm ? NW : 1;  // partitions per work-group
   const int ngrp = (p.parts + gparts - 1) / gparts;
   int part, z, grp = 0;  // part: per lane in the slot-partition mode
   if (compact_grid(p)) {
@@ -256,11 +248,13 @@ void decode_kernel(const DecodeParams p) {
   const bool fixed = p.part_tokens > 0;
   const bool ok = ctx > 0 && ctx_b <= maxctx;
   const int nparts = fixed ? (ok ? (ctx + p.part_tokens - 1) / p.part_tokens : 0) : p.parts;
-  const bool final_here = p.direct || (fixed && nparts <= 1);
+  // (fuse_final: a slot-partition work-group that covers every partition of
+  // its unit, GC == 1, also merges them and writes the output.)
+  const bool final_here = p.direct || (fixed && nparts <= 1) || p.fuse_final;
 
   if (!ok) {
     // Zero rows for an empty context, NaN rows for one longer than the table.
-    if (final_here && part == 0) {
+    if (final_here && (spm ? grp == 0 : part == 0)) {  // work-group uniform
       const float fillv = ctx <= 0 ? 0.0f : __builtin_nanf("");
       for (int idx = threadIdx.x; idx < GC * HP * D; idx += kDecodeThreads) {
         const int g = idx / (HP * D), dd = idx - g * (HP * D);
@@ -688,13 +682,38 @@ void decode_kernel(const DecodeParams p) {
     }
   };
 
+  // Combine the TPI slot streams of this wave (log-sum-exp rule).
+  auto combine_slots = [&]() {
+#pragma unroll
+    for (int off = LPT; off < 64; off <<= 1) {
+#pragma unroll
+      for (int g = 0; g < GC; ++g) {
+        const float mo = __shfl_xor(m[g], off, 64);
+        const float lo = __shfl_xor(l[g], off, 64);
+        const float mn = fmaxf(m[g], mo);
+        const float a = fast_exp2(m[g] - mn);
+        const float c = fast_exp2(mo - mn);
+        l[g] = l[g] * a + lo * c;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float ao = __shfl_xor(acc[g][e], off, 64);
+          acc[g][e] = acc[g][e] * a + ao * c;
+        }
+        m[g] = mn;
+      }
+    }
+  };
+
   if (spm) {
     // The work-group's block-table entries in one staged chunk (the host
     // enables the mode only when they fit).  Each slot streams its own
-    // partition, NI consecutive tokens per tile (a token past its end reads
-    // the masked safe row); the tile count is the chunk's, wave-uniform.
+    // partition of each round, NI consecutive tokens per tile (a token past
+    // its end reads the masked safe row); the tile count is the chunk's,
+    // wave-uniform, rounded up to even.  The two-tile pipeline runs on
+    // across rounds: a round's first tile is issued before the previous
+    // round's last is consumed.
+    const int cp = T0 < T1 ? (int)fastdiv((uint32_t)T0, p.bs_div) : 0;
     if (T0 < T1) {
-      const int cp = (int)fastdiv((uint32_t)T0, p.bs_div);
       const int np = (int)fastdiv((uint32_t)(T1 - 1), p.bs_div) + 1 - cp;
       if (bt_early && cp == pg_early) {
         static_assert(kBtChunk <= kDecodeThreads, "one prefetched entry per thread");
@@ -703,38 +722,110 @@ void decode_kernel(const DecodeParams p) {
         for (int i = threadIdx.x; i < np; i += kDecodeThreads) s_bt[i] = bt_row[cp + i];
       }
       __syncthreads();
-      auto iss = [&](int u, Tile& T) { issue_at([&](int i) { return t0 + u + i; }, cp, t1, T); };
-      const int nt = (chunk + NI - 1) / NI;
-      Tile A, B;
-      iss(0, A);
-      for (int j = 0; j + 1 < nt; j += 2) {
-        iss((j + 1) * NI, B);
-        consume(A);
-        iss((j + 2) * NI, A);
-        consume(B);
-      }
-      if (nt & 1) consume(A);
     }
-    rebase();
-    // This slot's partition: its partials from its lanes (dims dsub * VEC ..
-    // of head hl), m and l from those of dsub 0.
-    if (part < nparts) {
+    const int R = p.rounds;
+    const int nt = ((chunk + NI - 1) / NI + 1) & ~1;  // tiles per round (even)
+    // Fused output (GC == 1): each slot's partitions merged as they complete
+    // (log-sum-exp rule), then the wave's slots and the waves as below.  A
+    // bad block id poisons its own partition's partial and the output.
+    float mT = kNegBig, lT = 0.0f, aT[VEC];
 #pragma unroll
-      for (int g = 0; g < GC; ++g) {
-        if (g0 + g >= p.G) continue;
-        const int h = (kvh * HP + hl) * p.G + g0 + g;
-        const int64_t pidx = ((int64_t)b * p.H + h) * p.parts + part;
+    for (int e = 0; e < VEC; ++e) aT[e] = 0.0f;
+    int bad_all = 0;
+    int cr = 0;  // round being consumed
+    auto finish = [&]() __attribute__((always_inline)) {
+      rebase();
+      // This slot's partition: its partials from its lanes (dims dsub * VEC
+      // .. of head hl), m and l from those of dsub 0.
+      const int pr = part + cr * NW * TPI;
+      if (pr < nparts) {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) p.ws_acc[pidx * D + dsub * VEC + e] = acc[g][e] * p.vscale;
-        if (dsub == 0) {
-          p.ws_m[pidx] = m[g];
-          p.ws_l[pidx] = bad ? __builtin_nanf("") : l[g];
+        for (int g = 0; g < GC; ++g) {
+          if (g0 + g >= p.G) continue;
+          const int h = (kvh * HP + hl) * p.G + g0 + g;
+          const int64_t pidx = ((int64_t)b * p.H + h) * p.parts + pr;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) p.ws_acc[pidx * D + dsub * VEC + e] = acc[g][e] * p.vscale;
+          if (dsub == 0) {
+            p.ws_m[pidx] = m[g];
+            p.ws_l[pidx] = bad ? __builtin_nanf("") : l[g];
+          }
         }
       }
+      if constexpr (GC == 1) {
+        if (p.fuse_final) {
+          const float mn = fmaxf(mT, m[0]);
+          const float ca = fast_exp2(mT - mn), cb = fast_exp2(m[0] - mn);
+          lT = lT * ca + l[0] * cb;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) aT[e] = aT[e] * ca + acc[0][e] * cb;
+          mT = mn;
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < GC; ++g) {
+        m[g] = kNegBig;
+        mx[g] = kNegBig;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[g][e] = 0.0f;
+      }
+      m_own = kNegBig;
+      mx_own = kNegBig;
+      l_own = 0.0f;
+      bad_all |= bad;
+      bad = 0;
+      ++cr;
+    };
+    if (T0 < T1) {
+      // Issue position (round ir, token offset iu); past the last round a
+      // tile reads the masked safe row of the last round's partition.  Each
+      // tile carries the bad flag of its own loads, taken at consume time.
+      int ir = 0, iu = 0;
+      auto iss = [&](Tile& T, int& tb) __attribute__((always_inline)) {
+        const int pr = part + min(ir, R - 1) * NW * TPI;
+        const int r0 = min(pr * chunk, ctx), r1 = min(r0 + chunk, ctx);
+        const int u = ir < R ? iu : chunk;
+        const int keep = bad;
+        bad = 0;
+        issue_at([&](int i) { return r0 + u + i; }, cp, r1, T);
+        tb = bad;
+        bad = keep;
+        iu += NI;
+        if (iu >= nt * NI) {
+          iu = 0;
+          ++ir;
+        }
+      };
+      const int ntot = nt * R;
+      Tile A, B;
+      int ba, bb, cu = 0;
+      iss(A, ba);
+      for (int j = 0; j < ntot; j += 2) {
+        iss(B, bb);
+        bad |= ba;
+        consume(A);
+        iss(A, ba);
+        bad |= bb;
+        consume(B);
+        cu += 2;
+        if (cu == nt) {
+          finish();
+          cu = 0;
+        }
+      }
+    } else {
+      for (int r = 0; r < R; ++r) finish();  // empty partitions: m = -3e38, l = 0
     }
-    return;
-  }
-
+    bad = bad_all;
+    if constexpr (GC != 1) return;
+    if (!p.fuse_final) return;  // work-group uniform
+    m[0] = mT;
+    mx[0] = mT;
+    l[0] = lT;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[0][e] = aT[e];
+  } else {
   const bool fast = (p.BS % TPI) == 0 && (t0 % TPI) == 0;
   if (T0 < T1) {
     const int pg0 = (int)fastdiv((uint32_t)T0, p.bs_div);
@@ -793,27 +884,9 @@ void decode_kernel(const DecodeParams p) {
     }
   }
 
+  }  // slot-partition mode / plain sweep
   rebase();
-
-  // Combine the TPI slot streams of this wave (log-sum-exp rule).
-#pragma unroll
-  for (int off = LPT; off < 64; off <<= 1) {
-#pragma unroll
-    for (int g = 0; g < GC; ++g) {
-      const float mo = __shfl_xor(m[g], off, 64);
-      const float lo = __shfl_xor(l[g], off, 64);
-      const float mn = fmaxf(m[g], mo);
-      const float a = fast_exp2(m[g] - mn);
-      const float c = fast_exp2(mo - mn);
-      l[g] = l[g] * a + lo * c;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const float ao = __shfl_xor(acc[g][e], off, 64);
-        acc[g][e] = acc[g][e] * a + ao * c;
-      }
-      m[g] = mn;
-    }
-  }
+  combine_slots();
   if (wpm) {
     // This wave's partition complete: its partials straight from the lanes
     // of slot 0 (dims dsub * VEC .. of head hl), m and l from those of dsub 0.
@@ -916,16 +989,26 @@ hipError_t launch_decode_one(const DecodeParams& p, int64_t blocks, hipStream_t 
 template <typename KV, int D, int GC, int HP = 1>
 hipError_t launch_decode_dg(const DecodeParams& p0, hipStream_t stream) {
   DecodeParams p = p0;
-  // Short explicit partitions: one per token slot when every slot of a
-  // work-group has one (parts >= kDecodeWaves * TPI) and the work-group's
-  // pages fit one staged block-table chunk; else one per wave.
+  // Short explicit partitions.  A call whose host plan fuses
+  // (decode_fuse_rounds(), GC == 1) takes the slot-partition mode in rounds:
+  // one work-group per unit.  Otherwise one partition per token slot when
+  // every slot of a work-group has one (parts >= kDecodeWaves * TPI) and the
+  // work-group's pages fit one staged block-table chunk; else one per wave.
   constexpr int TPI = DecodeShapeOf<KV, D, GC, HP>::TPI;
-  if (p.wave_parts) {
+  const int fr = GC == 1 && p.fuse_final && p.wave_parts ? decode_fuse_rounds(p.parts, p.MB, p.BS, TPI) : 0;
+  p.fuse_final = fr > 0 ? 1 : 0;
+  p.rounds = 1;
+  if (fr > 0) {
+    p.wave_parts = kSlotPart;
+    p.rounds = fr;
+    t_decode_fused = 1;
+  } else if (p.wave_parts) {
     const int64_t chunk_max = ((int64_t)p.MB * p.BS + p.parts - 1) / p.parts;
     const int64_t pages = ((int64_t)kDecodeWaves * TPI * chunk_max + p.BS - 1) / p.BS + 1;
     p.wave_parts = p.parts >= kDecodeWaves * TPI && pages <= kBtChunk ? kSlotPart : kWavePart;
   }
-  const int64_t gparts = p.wave_parts == kSlotPart ? kDecodeWaves * TPI : p.wave_parts ? kDecodeWaves : 1;
+  const int64_t gparts = p.wave_parts == kSlotPart ? (int64_t)kDecodeWaves * TPI * p.rounds
+                                                   : p.wave_parts ? kDecodeWaves : 1;
   const int64_t groups = (p.parts + gparts - 1) / gparts;
   const int64_t blocks = (int64_t)p.B * p.Sq * (p.HKV / HP) * p.head_chunks * groups;
   constexpr int PTS = pair_types<KV>::value;

@@ -1,0 +1,190 @@
+"""GPU parity of the fused explicit split: a paged_attention_v3 call with an
+explicit num_splits of short partitions, one query head per work-group's head
+chunk, and a grid of one work-group per (sequence, head) that fills the GPU
+runs as ONE kernel launch.  Each work-group serves every partition of its
+sequence and head in rounds of one partition per token slot (4 waves x TPI
+slots, TPI = token rows per load instruction), writes each
+partition's partials to the workspace as the split pass does
+(kernels/paged_attn_v3.cu:33-123), and merges them into the output by the
+reduce's log-sum-exp rule (kernels/paged_attn_v3.cu:128-166) itself.
+
+Checked against the oracle: the output, the
+partials' semantics (partition bounds bit-exact through K = 0, where every
+score is 0 and l is the partition's token count), a bad block id poisoning
+only its row, and the two-launch path (pa_v3_partition + pa_v3_reduce) on
+the same inputs.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _helpers import ATOL32, RTOL32, close, decode_case, dev_inputs, to_host
+
+pytestmark = pytest.mark.gpu
+
+WAVES = 4          # waves per work-group
+MAX_ROUNDS = 8     # most rounds per work-group
+BT_CHUNK = 256     # block-table entries one work-group stages
+WAVE_PART_TOKENS = 256  # longest explicit partition of the short-split modes
+
+
+def expect_fused(pa, B, H, D, kv_bytes, MB, BS, S, dev):
+    """The host plan's fuse rule restated for these grids (one work-group per
+    (row, head) at the narrowest packing, just filling the GPU): explicit
+    short partitions, at least one per token slot, rounds and pages within
+    bounds."""
+    maxctx = MB * BS
+    chunk = -(-maxctx // S)
+    hp = 2 if D * kv_bytes < 128 and H % 2 == 0 else 1
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    if S < 2 or chunk > WAVE_PART_TOKENS or B * (H // hp) < cus:
+        return False
+    vec = 8 if kv_bytes == 1 else 16 // kv_bytes
+    tpi = max(1, 64 // (D * hp // vec))
+    slots = WAVES * tpi
+    R = -(-S // slots)
+    pages = -(-(R * slots * chunk) // BS) + 1
+    return S >= slots and R <= MAX_ROUNDS and pages <= BT_CHUNK
+
+
+def two_launch(pa, out, q, k, v, bt, ctx, scale, S, ws):
+    V = pa.view
+    st = torch.cuda.current_stream().cuda_stream
+    pa.check(pa.lib().pa_v3_partition(C.byref(V(out)), C.byref(V(q)), C.byref(V(k)), C.byref(V(v)),
+                                      C.byref(V(bt)), C.byref(V(ctx)), scale, S, ws.data_ptr(), ws.numel(), st))
+    pa.check(pa.lib().pa_v3_reduce(C.byref(V(out)), C.byref(V(q)), C.byref(V(k)), C.byref(V(bt)),
+                                   C.byref(V(ctx)), S, ws.data_ptr(), ws.numel(), st))
+
+
+def grid_rows(dev, H, lo=1):
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    return -(-cus * lo // H)
+
+
+CASES = [  # kv, D, BS, MB, S
+    ("f16", 64, 16, 64, 64),    # config 2's shape of split: 2 rounds of 32 16-token partitions
+    ("f16", 64, 16, 64, 40),    # ragged rounds: the second has 8 partitions
+    ("bf16", 128, 16, 32, 24),  # 16 slots: 2 rounds, 22-token partitions
+    ("f32", 64, 8, 64, 48),     # 3 rounds of 11-token partitions
+    ("f16", 256, 32, 16, 64),   # 8 slots: 8 rounds
+    ("f16", 32, 16, 32, 64),    # two heads packed per work-group (64-byte rows)
+    ("bf16", 64, 1, 64, 64),    # one token per page and per partition
+    ("f16", 64, 5, 50, 33),     # page size not a multiple of the token slots
+]
+
+
+@pytest.mark.parametrize("kv,D,BS,MB,S", CASES)
+def test_fused_split_matches_oracle(pa, dev, kv, D, BS, MB, S):
+    """Ragged contexts (empty, one token, the whole table, beyond the table,
+    random) through the one-launch fused split, against the oracle and the
+    two-launch split on the same inputs."""
+    H = 8
+    kvb = {"f16": 2, "bf16": 2, "f32": 4}[kv]
+    lo = 2 if D * kvb < 128 else 1
+    B = grid_rows(dev, H, lo)
+    maxctx = MB * BS
+    rng = np.random.default_rng(D * 131 + S)
+    ctx = rng.integers(1, maxctx + 1, size=B).astype(np.int32)
+    ctx[:4] = [0, 1, maxctx, maxctx - 1]
+    inp = decode_case(B, H, H, D, BS, ctx.tolist(), seed=70 + S, kv=kv, q=kv, mb=MB)
+    q, k, v, bt, _ = dev_inputs(inp, dev)
+    ctx_run = inp["ctx"].copy()
+    ctx_run[4] = maxctx + 1  # beyond the table: NaN row
+    cd = torch.from_numpy(ctx_run).to(dev)
+    assert expect_fused(pa, B, H, D, kvb, MB, BS, S, dev)
+    got = to_host(pa.paged_attention_v3(q, k, v, bt, cd, 0.125, S))
+    launched = pa.last_launch()
+    assert "reduce_kernel" not in launched and launched.count("decode_kernel") == 1, launched
+    assert np.all(got[0] == 0.0)
+    assert np.all(np.isnan(got[4]))
+    want = oracle.decode(inp["q_f32"], inp["k"], inp["v"], inp["bt"], ctx_run, 0.125, kv)
+    tol = dict(atol=ATOL32, rtol=RTOL32) if kv == "f32" else {}
+    live = np.ones(B, bool)
+    live[[0, 4]] = False
+    close(got[live], want[live], **tol)
+    # The two-launch split over the same partitions.
+    ws = torch.zeros(pa.workspace_size(q, k, bt, S), dtype=torch.uint8, device=dev)
+    out2 = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+    two_launch(pa, out2, q, k, v, bt, cd, 0.125, S, ws)
+    torch.cuda.synchronize()
+    close(got[live], to_host(out2)[live], **tol)
+
+
+@pytest.mark.parametrize("S", [16, 33, 64])
+def test_fused_split_partials_bit_exact(pa, dev, S):
+    """With K = 0 every score is 0: after the one-launch call the workspace
+    holds each partition's l = its token count exactly and m = 0 (empty
+    partitions m = -3e38, l = 0), the reference's partition bounds
+    [s*chunk, min((s+1)*chunk, ctx)), chunk = ceil(ctx/S)
+    (kernels/paged_attn_v3.cu:65-68); the output is the plain mean of V."""
+    H, D, BS, MB = 8, 64, 16, 64
+    B = grid_rows(dev, H)
+    maxctx = MB * BS
+    rng = np.random.default_rng(S)
+    ctx = rng.integers(1, maxctx + 1, size=B).astype(np.int32)
+    ctx[:5] = [1, 2, 7, S + 1, maxctx]
+    inp = decode_case(B, H, H, D, BS, ctx.tolist(), seed=5, kv="f32", q="f32", mb=MB)
+    q, _, v, bt, cd = dev_inputs(inp, dev)
+    k = torch.zeros_like(v)
+    need = pa.workspace_size(q, k, bt, S)
+    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=dev)
+    got = to_host(pa.paged_attention_v3(q, k, v, bt, cd, 1.0, S, workspace=ws))
+    assert "reduce_kernel" not in pa.last_launch(), pa.last_launch()
+    rows = B * H * S
+    up = lambda x: (x + 255) // 256 * 256
+    w = ws.cpu().numpy()
+    m = w[up(rows * D * 4): up(rows * D * 4) + rows * 4].view(np.float32).reshape(B, H, S)
+    l = w[up(rows * D * 4) + up(rows * 4):][:rows * 4].view(np.float32).reshape(B, H, S)
+    for b in range(B):
+        for s in range(S):
+            st, en = oracle.partition_bounds(int(ctx[b]), S, s)
+            n = max(0, en - st)
+            assert np.all(l[b, :, s] == n), (b, s, l[b, :, s], n)
+            assert np.all(m[b, :, s] == (np.float32(-3.0e38) if n == 0 else 0.0)), (b, s, m[b, :, s])
+    want = oracle.decode(inp["q_f32"], np.zeros_like(inp["k"]), inp["v"], inp["bt"], inp["ctx"], 1.0, "f32")
+    close(got, want, atol=ATOL32, rtol=RTOL32)
+
+
+def test_fused_split_bad_block_id(pa, dev):
+    """A block id outside the pool in one sequence's table: that row is NaN
+    (every head), every other row matches the oracle, and the partials of
+    the partition holding the bad page carry l = NaN while the sequence's
+    other partitions stay finite."""
+    H, D, BS, MB, S = 8, 64, 16, 64, 64
+    B = grid_rows(dev, H)
+    maxctx = MB * BS
+    inp = decode_case(B, H, H, D, BS, [maxctx] * B, seed=9, kv="f16", q="f16", mb=MB)
+    q, k, v, _, cd = dev_inputs(inp, dev)
+    bt_h = inp["bt"].copy()
+    nb = inp["k"].shape[0]
+    bt_h[3, 10] = nb + 5  # page 10 = tokens 160..175: partition 10 of 16-token partitions
+    bt = torch.from_numpy(bt_h).to(dev)
+    ws = torch.zeros(pa.workspace_size(q, k, bt, S), dtype=torch.uint8, device=dev)
+    got = to_host(pa.paged_attention_v3(q, k, v, bt, cd, 0.125, S, workspace=ws))
+    assert "reduce_kernel" not in pa.last_launch(), pa.last_launch()
+    assert np.all(np.isnan(got[3]))
+    keep = np.arange(B) != 3
+    want = oracle.decode(inp["q_f32"][keep], inp["k"], inp["v"], inp["bt"][keep], inp["ctx"][keep], 0.125, "f16")
+    close(got[keep], want)
+    rows = B * H * S
+    up = lambda x: (x + 255) // 256 * 256
+    w = ws.cpu().numpy()
+    l = w[up(rows * D * 4) + up(rows * 4):][:rows * 4].view(np.float32).reshape(B, H, S)
+    assert np.all(np.isnan(l[3, :, 10]))
+    assert np.all(np.isfinite(np.delete(l[3], 10, axis=1)))
+    assert np.all(np.isfinite(l[keep]))
+
+
+def test_small_grid_keeps_two_launches(pa, dev):
+    """A grid of one work-group per (row, head) that would not fill the GPU
+    keeps the partition kernel and the reduce (both launched by one call)."""
+    H, D, BS, MB, S = 8, 64, 16, 64, 64
+    B = 2
+    inp = decode_case(B, H, H, D, BS, [MB * BS, 300], seed=11, kv="f16", q="f16", mb=MB)
+    q, k, v, bt, cd = dev_inputs(inp, dev)
+    got = to_host(pa.paged_attention_v3(q, k, v, bt, cd, 0.125, S))
+    assert "reduce_kernel" in pa.last_launch(), pa.last_launch()
+    close(got, oracle.decode(inp["q_f32"], inp["k"], inp["v"], inp["bt"], inp["ctx"], 0.125, "f16"))
