@@ -736,9 +736,12 @@ void decode_kernel(const DecodeParams p) {
     auto finish = [&]() __attribute__((always_inline)) {
       rebase();
       // This slot's partition: its partials from its lanes (dims dsub * VEC
-      // .. of head hl), m and l from those of dsub 0.
+      // .. of head hl), m and l from those of dsub 0.  The fused form keeps
+      // them in registers only: the workspace is the split's scratch, and
+      // the partials' writes (3 % of the bytes, 4-byte m and l stores among
+      // them) took config 2 at 64 splits from 0.77 to 0.68 of 8 TB/s.
       const int pr = part + cr * NW * TPI;
-      if (pr < nparts) {
+      if (pr < nparts && !p.fuse_final) {
 #pragma unroll
         for (int g = 0; g < GC; ++g) {
           if (g0 + g >= p.G) continue;

@@ -115,6 +115,11 @@ int paged_attention_v2(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t
  * num_splits <= 0: the library plans fixed-size partitions from MB*BS, the
  *   batch size and the device's CU count (see pa_plan_partitions); when the
  *   batch alone fills the GPU no split and no reduce launch happen.
+ * An explicit split into short partitions (at most 256 tokens at MB*BS),
+ * with one query head per work-group head chunk (MHA, or odd GQA group
+ * sizes above 8), whose one-work-group-per-(sequence, head) grid fills the GPU,
+ * runs fused: one launch computes every partition and merges them by the
+ * same rule in registers, and the workspace is not written.
  * workspace must be device memory of at least
  *   paged_attention_v3_workspace_size(...) bytes (NULL allowed when that is 0). */
 int paged_attention_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k_cache,
@@ -131,7 +136,8 @@ size_t paged_attention_v3_workspace_size(const pa_tensor_t* q, const pa_tensor_t
  * or interleave them.  pa_v3_partition writes per-partition softmax state
  * into the workspace (or, for sequences that fit one partition, the final
  * output); pa_v3_reduce merges it.  Calling both back to back on one stream
- * is exactly paged_attention_v3.
+ * computes what paged_attention_v3 computes: the same partitions and merge
+ * rule (the one-call form may run them fused, as described there).
  * Workspace layout for a plan with P partitions per sequence:
  *   float acc[B][H][P][D]   un-normalised sum_j p_j v_j   (kernels/paged_attn_v3.cu:113-122)
  *   float m  [B][H][P]      running max, in log2 units (score * scale * log2 e)

@@ -3,16 +3,18 @@ explicit num_splits of short partitions, one query head per work-group's head
 chunk, and a grid of one work-group per (sequence, head) that fills the GPU
 runs as ONE kernel launch.  Each work-group serves every partition of its
 sequence and head in rounds of one partition per token slot (4 waves x TPI
-slots, TPI = token rows per load instruction), writes each
-partition's partials to the workspace as the split pass does
-(kernels/paged_attn_v3.cu:33-123), and merges them into the output by the
-reduce's log-sum-exp rule (kernels/paged_attn_v3.cu:128-166) itself.
+slots, TPI = token rows per load instruction), computes each partition's
+partials as the split pass does (kernels/paged_attn_v3.cu:33-123) and merges
+them into the output by the reduce's log-sum-exp rule
+(kernels/paged_attn_v3.cu:128-166) in registers: the partials are never
+written (the workspace is the split's scratch; the reference allocates its
+partials inside the call and never returns them, paged_attn_v3.cu:221-224).
+The two-launch path's partials keep their own bit-exact partition test.
 
-Checked against the oracle: the output, the
-partials' semantics (partition bounds bit-exact through K = 0, where every
-score is 0 and l is the partition's token count), a bad block id poisoning
-only its row, and the two-launch path (pa_v3_partition + pa_v3_reduce) on
-the same inputs.
+Checked against the oracle: the output, equal scores
+(K = 0), a bad block id poisoning only its row, the workspace left
+untouched, and the two-launch path (pa_v3_partition + pa_v3_reduce) on the
+same inputs.
 """
 import ctypes as C
 
@@ -114,12 +116,11 @@ def test_fused_split_matches_oracle(pa, dev, kv, D, BS, MB, S):
 
 
 @pytest.mark.parametrize("S", [16, 33, 64])
-def test_fused_split_partials_bit_exact(pa, dev, S):
-    """With K = 0 every score is 0: after the one-launch call the workspace
-    holds each partition's l = its token count exactly and m = 0 (empty
-    partitions m = -3e38, l = 0), the reference's partition bounds
-    [s*chunk, min((s+1)*chunk, ctx)), chunk = ceil(ctx/S)
-    (kernels/paged_attn_v3.cu:65-68); the output is the plain mean of V."""
+def test_fused_split_equal_scores(pa, dev, S):
+    """With K = 0 every score is 0, every partition's maximum the same: the
+    output is the plain mean of V over each row's context, whatever its
+    partitions (empty ones included: ctx 1, 2, 7 leave most of the 16-64
+    partitions empty).  The workspace (filled with 0xFF) is left untouched."""
     H, D, BS, MB = 8, 64, 16, 64
     B = grid_rows(dev, H)
     maxctx = MB * BS
@@ -133,26 +134,14 @@ def test_fused_split_partials_bit_exact(pa, dev, S):
     ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=dev)
     got = to_host(pa.paged_attention_v3(q, k, v, bt, cd, 1.0, S, workspace=ws))
     assert "reduce_kernel" not in pa.last_launch(), pa.last_launch()
-    rows = B * H * S
-    up = lambda x: (x + 255) // 256 * 256
-    w = ws.cpu().numpy()
-    m = w[up(rows * D * 4): up(rows * D * 4) + rows * 4].view(np.float32).reshape(B, H, S)
-    l = w[up(rows * D * 4) + up(rows * 4):][:rows * 4].view(np.float32).reshape(B, H, S)
-    for b in range(B):
-        for s in range(S):
-            st, en = oracle.partition_bounds(int(ctx[b]), S, s)
-            n = max(0, en - st)
-            assert np.all(l[b, :, s] == n), (b, s, l[b, :, s], n)
-            assert np.all(m[b, :, s] == (np.float32(-3.0e38) if n == 0 else 0.0)), (b, s, m[b, :, s])
+    assert bool((ws == 0xFF).all())
     want = oracle.decode(inp["q_f32"], np.zeros_like(inp["k"]), inp["v"], inp["bt"], inp["ctx"], 1.0, "f32")
     close(got, want, atol=ATOL32, rtol=RTOL32)
 
 
 def test_fused_split_bad_block_id(pa, dev):
     """A block id outside the pool in one sequence's table: that row is NaN
-    (every head), every other row matches the oracle, and the partials of
-    the partition holding the bad page carry l = NaN while the sequence's
-    other partitions stay finite."""
+    (every head) and every other row matches the oracle."""
     H, D, BS, MB, S = 8, 64, 16, 64, 64
     B = grid_rows(dev, H)
     maxctx = MB * BS
@@ -162,20 +151,12 @@ def test_fused_split_bad_block_id(pa, dev):
     nb = inp["k"].shape[0]
     bt_h[3, 10] = nb + 5  # page 10 = tokens 160..175: partition 10 of 16-token partitions
     bt = torch.from_numpy(bt_h).to(dev)
-    ws = torch.zeros(pa.workspace_size(q, k, bt, S), dtype=torch.uint8, device=dev)
-    got = to_host(pa.paged_attention_v3(q, k, v, bt, cd, 0.125, S, workspace=ws))
+    got = to_host(pa.paged_attention_v3(q, k, v, bt, cd, 0.125, S))
     assert "reduce_kernel" not in pa.last_launch(), pa.last_launch()
     assert np.all(np.isnan(got[3]))
     keep = np.arange(B) != 3
     want = oracle.decode(inp["q_f32"][keep], inp["k"], inp["v"], inp["bt"][keep], inp["ctx"][keep], 0.125, "f16")
     close(got[keep], want)
-    rows = B * H * S
-    up = lambda x: (x + 255) // 256 * 256
-    w = ws.cpu().numpy()
-    l = w[up(rows * D * 4) + up(rows * 4):][:rows * 4].view(np.float32).reshape(B, H, S)
-    assert np.all(np.isnan(l[3, :, 10]))
-    assert np.all(np.isfinite(np.delete(l[3], 10, axis=1)))
-    assert np.all(np.isfinite(l[keep]))
 
 
 def test_small_grid_keeps_two_launches(pa, dev):
