@@ -441,17 +441,46 @@ WRITE_CFG = {
 }
 
 
+def copy_reference_ms(nbytes, steps, copies=8):
+    """ms per launch of torch's own contiguous device copy moving the same
+    bytes (nbytes / 2 read, nbytes / 2 written), rotated over `copies`
+    buffer pairs like the write workloads: the device's rate for a plain copy
+    launch of this size, measured in the same process."""
+    dev = torch.device("cuda:0")
+    n = int(nbytes // 4)  # 16-bit elements per side
+    srcs = [torch.ones(n, device=dev, dtype=torch.float16) for _ in range(copies)]
+    dsts = [torch.empty_like(x) for x in srcs]
+    stream = torch.cuda.current_stream()
+    for i in range(20):
+        dsts[i % copies].copy_(srcs[i % copies])
+    torch.cuda.synchronize()
+    reps = []
+    for _ in range(REPEATS):
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for i in range(steps):
+            dsts[i % copies].copy_(srcs[i % copies])
+        t1.record(stream)
+        torch.cuda.synchronize()
+        reps.append(t0.elapsed_time(t1) / steps)
+    return float(np.median(reps))
+
+
 def write_record(work, steps, warmup):
     chk, kernels = check_write(work)
     if not chk["ok"]:
         return failed_record(work.name, chk, kernels)
     ms, kms, _ = timed(work, steps, warmup)
     gbs = work.bytes / (kms * 1e-3) / 1e9
+    cms = copy_reference_ms(work.bytes, steps)
     return {
         "workload": work.name, "value": round(gbs, 1), "unit": "GB/s",
         "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4), "ms_per_step": round(ms, 5),
         "kernel_ms": round(kms, 5), "bytes_per_step": work.bytes, "dtype": str(work.dtype).replace("torch.", ""),
         "cache_dtype": str(work.cache_dtype).replace("torch.", ""),
+        "plain_copy_same_bytes": {"ms": round(cms, 5), "GBs": round(work.bytes / (cms * 1e-3) / 1e9, 1),
+                                  "what": "torch copy_ of one contiguous buffer, same bytes moved, 8 rotated pairs"},
         "kernels": kernels, "check": chk,
     }
 
