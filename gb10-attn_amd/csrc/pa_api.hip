@@ -178,6 +178,17 @@ struct PlanKnobs {
   int64_t min_part = 256;
   int64_t min_part_tiny = 64;
   int64_t max_part = 2048;
+  // A split pays for its reduce launch only when the unsplit work-groups'
+  // streams are long: contexts (in 64-element rows) of at least
+  // split_min_tokens, and ctx^2 * CUs >= split_pay * units.  Measured on 256
+  // CUs, GPT-2 heads (D = 64, fp16), B = 1-32 x ctx 256-1536, whole calls
+  // back to back: the direct launch won below 1024 tokens at every B (B = 1
+  // ctx 512: 10.0 vs 11.0 us; B = 16 ctx 512: 11.1 vs 14.9 us) and up to
+  // 1536 tokens at B = 16 (20.4 vs 22.5 us); the split won from 1024 tokens
+  // at B <= 4 (B = 1 ctx 1024: 11.6 vs 14.0 us), from 1536 at B = 8 (17.4 vs
+  // 19.1 us) and at B = 16 ctx 2048 (+3 %).
+  int64_t split_min_tokens = 1024;
+  int64_t split_pay = 16384 * 256;
 };
 
 const PlanKnobs& knobs() {
@@ -578,12 +589,18 @@ int pa_plan_partitions(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads
   if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads || max_context < 0 ||
       num_compute_units <= 0)
     return fail(PA_ERR_INVALID_ARGUMENT, "invalid planning arguments");
-  (void)head_dim;
   const PlanKnobs& kn = knobs();
   const int64_t G = num_heads / num_kv_heads;
   const int64_t gc = decode_heads_per_wg((int)G);
   const int64_t units = std::max<int64_t>(1, num_seqs * num_kv_heads * ((G + gc - 1) / gc));
   const int64_t target = num_compute_units * kn.wgs_per_cu;
+  const double ctx_rows = (double)max_context * (double)std::max<int64_t>(head_dim, 1) / 64.0;
+  if (ctx_rows < (double)kn.split_min_tokens ||
+      ctx_rows * ctx_rows * (double)num_compute_units < (double)kn.split_pay * (double)units) {
+    *partition_tokens = std::max<int64_t>(max_context, 1);
+    *num_partitions = 1;
+    return PA_OK;
+  }
   int64_t S = (target + units - 1) / units;                             // fill the GPU
   S = std::max(S, (max_context + kn.max_part - 1) / kn.max_part);       // bound partition length
   // Tiny grids (the units with partitions of min_part tokens still cannot

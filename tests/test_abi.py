@@ -184,10 +184,19 @@ def test_plan_partitions(pa):
     # tiny problem: no split
     assert pa.plan_partitions(1, 1, 1, 64, 100, 256) == (100, 1)
     # tiny grids (a few short sequences, far from filling 256 CUs): 64- or 128-token partitions
-    # instead of 256, so that more work-groups stream at once (B=1 ctx=512: 8 x 64; B=4 ctx=2048: 16 x 128)
-    assert pa.plan_partitions(1, 12, 12, 64, 512, 256) == (64, 8)
+    # instead of 256, so that more work-groups stream at once (B=4 ctx=2048: 16 x 128)
     assert pa.plan_partitions(4, 12, 12, 64, 2048, 256) == (128, 16)
+    assert pa.plan_partitions(1, 12, 12, 64, 1024, 256) == (64, 16)
+    assert pa.plan_partitions(8, 12, 12, 64, 1536, 256)[1] > 1
     assert pa.plan_partitions(16, 12, 12, 64, 2048, 256) == (512, 4)
+    # ... but a split must pay for its reduce launch: short contexts, or grids whose
+    # unsplit streams are short for their width, run direct (one launch)
+    assert pa.plan_partitions(1, 12, 12, 64, 512, 256) == (512, 1)
+    assert pa.plan_partitions(32, 12, 12, 64, 768, 256) == (768, 1)
+    assert pa.plan_partitions(16, 12, 12, 64, 1536, 256) == (1536, 1)
+    assert pa.plan_partitions(32, 12, 12, 64, 2048, 256) == (2048, 1)
+    # (head_dim counts: 128-element rows are twice the bytes per token)
+    assert pa.plan_partitions(1, 12, 12, 128, 512, 256)[1] > 1
     for B in (1, 2, 7, 64, 300):
         for ctx in (1, 31, 256, 4096, 100000):
             ptok, n = pa.plan_partitions(B, 32, 8, 128, ctx, 256)
