@@ -181,14 +181,16 @@ struct PlanKnobs {
   // A split pays for its reduce launch only when the unsplit work-groups'
   // streams are long: contexts (in 64-element rows) of at least
   // split_min_tokens, and ctx^2 * CUs >= split_pay * units.  Measured on 256
-  // CUs, GPT-2 heads (D = 64, fp16), B = 1-32 x ctx 256-1536, whole calls
-  // back to back: the direct launch won below 1024 tokens at every B (B = 1
-  // ctx 512: 10.0 vs 11.0 us; B = 16 ctx 512: 11.1 vs 14.9 us) and up to
-  // 1536 tokens at B = 16 (20.4 vs 22.5 us); the split won from 1024 tokens
-  // at B <= 4 (B = 1 ctx 1024: 11.6 vs 14.0 us), from 1536 at B = 8 (17.4 vs
-  // 19.1 us) and at B = 16 ctx 2048 (+3 %).
+  // CUs, GPT-2 heads (D = 64, fp16), B = 1-48 x ctx 256-2048, whole calls
+  // back to back: the unsplit launch won below 1024 tokens at every B (B = 1
+  // ctx 512: 10.0 vs 11.0 us; B = 16 ctx 512: 11.1 vs 14.9 us), at 1024 from
+  // B = 8 on (equal at 8; B = 32: 22.6 vs 25.9 us), at 1536 from B = 16 on
+  // (20.4 vs 22.5 us) and at 2048 from B = 32 on (38.6 vs 41.5 us); the split
+  // won from 1024 tokens at B <= 4 (B = 1 ctx 1024: 11.6 vs 14.0 us) and at
+  // 1536 at B = 8 (17.4 vs 19.2 us); B = 16 at 2048 sits at the boundary
+  // (either by 3-4 %, run to run).
   int64_t split_min_tokens = 1024;
-  int64_t split_pay = 16384 * 256;
+  int64_t split_pay = 21845 * 256;
 };
 
 const PlanKnobs& knobs() {
@@ -362,9 +364,13 @@ int make_plan(const DecodeParams& p, int gc, int kv_bytes, int64_t num_splits, P
   // A grid that does not fill the GPU even unpacked keeps every work-group
   // it can get (latency-bound: more loads in flight beat wider rows).
   const bool fills = (int64_t)p.B * p.Sq * (p.HKV / lo) * nparts >= (int64_t)cus * knobs().wgs_per_cu;
+  // The packed grid must fill the GPU too (an unsplit plan at the packed
+  // width can leave it short: config 2 at two heads per work-group would be
+  // 384 work-groups on 256 CUs).
   for (int c = hi; fills && c > lo; c /= 2) {
     int64_t pt = 0;
-    if (parts_for(c, &pt) == nparts && pt == ptok) {
+    if (parts_for(c, &pt) == nparts && pt == ptok &&
+        (int64_t)p.B * p.Sq * (p.HKV / c) * nparts >= (int64_t)cus * knobs().wgs_per_cu) {
       hp = c;
       break;
     }

@@ -1347,20 +1347,30 @@ static hipError_t launch_pp(const PrefillParams& p, hipStream_t stream) {
 // (the reference's 512-token chunk at context 2048: 192 work-groups, +19 %).
 // Above that, twice the tiles cost more than the shorter chains save
 // (config 4a, 768 work-groups: -17 %).
+// The choice counts the work-groups that have rows to serve: a uniform
+// batch's B * ceil(S / rows) per head; a variable-length batch brings T rows
+// in all (its grid is sized by the longest sequence, and the work-groups past
+// a sequence's rows exit at once), so about ceil(T / rows) of its blocks carry
+// work.  (A mixed batch of 64 decode rows and four 256-row chunks had taken
+// the 8-wave kernel for its 816-block grid: 48 blocks with rows, on 256 CUs.)
 template <typename KV, int D>
 static hipError_t launch_pf(const PrefillParams& p, hipStream_t stream) {
   if constexpr (PfShape<D>::MT == 2) {
     static std::atomic<int64_t> cache[64];
     int64_t cus = 0, per_cu = 0;
     residency(prefill_mfma_kernel<KV, D, false, false>, cache, &cus, &per_cu);
-    const int64_t plain = (int64_t)p.B * p.H * ((p.S + PfShape<D>::QB - 1) / PfShape<D>::QB);
+    auto busy = [&](int rows) {
+      const int64_t grid = (int64_t)p.B * ((p.S + rows - 1) / rows);
+      return (int64_t)p.H * (p.cu_q ? std::min<int64_t>(grid, (p.q_total + rows - 1) / rows) : grid);
+    };
+    const int64_t plain = busy(PfShape<D>::QB);
     if (cus > 0 && plain < cus)
       return p.q_split ? launch_pf_q<KV, D, true, true>(p, stream) : launch_pf_q<KV, D, false, true>(p, stream);
     // The 8-wave kernel (one work-group per CU) for grids of at least two
     // of its work-groups per CU; below that its 256-row blocks leave CUs
     // idle at the end of the launch (config 4a: 384 work-groups, -20 %).
     if constexpr (KV::kCode == kF16 || KV::kCode == kBF16) {
-      const int64_t pp_units = (int64_t)p.B * p.H * ((p.S + kPpRows - 1) / kPpRows);
+      const int64_t pp_units = busy(kPpRows);
       if (!p.q_split && p.MB <= kPfBtStage && cus > 0 && pp_units >= 2 * cus) return launch_pp<KV, D>(p, stream);
     }
   }

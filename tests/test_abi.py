@@ -194,6 +194,7 @@ def test_plan_partitions(pa):
     assert pa.plan_partitions(1, 12, 12, 64, 512, 256) == (512, 1)
     assert pa.plan_partitions(32, 12, 12, 64, 768, 256) == (768, 1)
     assert pa.plan_partitions(16, 12, 12, 64, 1536, 256) == (1536, 1)
+    assert pa.plan_partitions(32, 12, 12, 64, 1024, 256) == (1024, 1)
     assert pa.plan_partitions(32, 12, 12, 64, 2048, 256) == (2048, 1)
     # (head_dim counts: 128-element rows are twice the bytes per token)
     assert pa.plan_partitions(1, 12, 12, 128, 512, 256)[1] > 1

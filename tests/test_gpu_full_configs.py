@@ -91,6 +91,9 @@ def test_config2_full(pa, dev):
     for ns in (0, 64):
         got = pa.paged_attention_v3(q, k, v, bt, cl, scale, ns, out_dtype=torch.float32)
         close(to_host(got), want)
+        # Both run as one launch of one head per work-group (768 work-groups on
+        # 256 CUs): the plan unsplit, the reference's count fused.
+        assert pa.last_launch() == "pa::decode_kernel<pa::KvF16, 64, 1, 1, 1>", (ns, pa.last_launch())
     got = pa.paged_attention_v3(q, k, v, bt, cl, scale, 0, out_dtype=torch.float16)
     k2, v2, bt2 = permuted(k, v, bt, 23)
     got2 = pa.paged_attention_v3(q, k2, v2, bt2, cl, scale, 0, out_dtype=torch.float16)
