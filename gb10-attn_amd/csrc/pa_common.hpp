@@ -105,6 +105,7 @@ struct PrefillParams {
   const int32_t* cu_q;  // variable-length batches: [B + 1] row offsets into [T, H, D] q/out (else null)
   int64_t q_total;      // T (variable-length batches)
   int32_t skip_single;  // variable-length batches: sequences of one row are served by the decode kernel
+  int32_t vl_compact;   // variable-length batches (B <= kVlMaxSeqs): the grid holds only units with rows
   int32_t q_split;   // q is not exactly the KV type: add a low-part product
   FastDiv bs_div;
   float qscale;      // |scale| * log2(e), or 1 when scale == 0 (always positive)

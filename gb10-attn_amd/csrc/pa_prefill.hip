@@ -124,6 +124,7 @@ __device__ inline void load8f(const void* q, int dtype, int64_t idx, float (&x)[
 }
 
 constexpr int kPfThreads = 256;   // 4 waves
+constexpr int kVlMaxSeqs = 256;   // variable-length batches numbered compactly (four per lane)
 constexpr int kPfBtStage = 1024;  // block-table entries staged in LDS
 constexpr float kLazyRescale = 8.0f;  // raise the running max only past 2^8
 
@@ -249,15 +250,65 @@ void prefill_mfma_kernel(const PrefillParams p) {
   // stay on one XCD's L2.
   const int nq = p.q_tiles;
   const int64_t nbh = (int64_t)p.B * p.H;
-  int64_t x = blockIdx.x;
-  if (p.wg_cus > 0) {
-    const int64_t C = p.wg_cus, g = x / C, j = x - g * C;
-    if ((g & 1) && (g + 1) * C <= nbh * nq) x = g * C + (C % 8 == 0 ? C - 8 - (j & ~(int64_t)7) + (j & 7) : C - 1 - j);
+  int qt, h, b;
+  if (p.vl_compact) {
+    // Variable-length batch, compacted grid: the work-groups take only the
+    // (query block, sequence, head) units that have rows -- query blocks
+    // from the last (longest) down, then sequences, then heads -- and those
+    // past the last unit exit.  A grid sized by the longest sequence would
+    // dispatch a work-group for every block of every sequence, most of them
+    // (decode rows of a mixed batch, blocks past a short sequence's rows)
+    // exiting only after a memory round trip, and spread the working ones
+    // across the launch.  Per-sequence block counts sit in the lanes
+    // (kVlMaxSeqs / 64 per lane); each level costs one ballot per chunk.
+    int nbk[kVlMaxSeqs / 64];
+#pragma unroll
+    for (int c = 0; c < kVlMaxSeqs / 64; ++c) {
+      const int i = c * 64 + lane;
+      nbk[c] = 0;
+      if (i < p.B) {
+        const int qa = p.cu_q[i], qb = p.cu_q[i + 1];
+        int len = qa >= 0 && qb >= qa && (int64_t)qb <= p.q_total ? qb - qa : 0;
+        if (p.skip_single && len == 1) len = 0;
+        nbk[c] = (min(len, p.S) + QB - 1) / QB;
+      }
+    }
+    int64_t rem = blockIdx.x;
+    int fb = -1, ft = 0, fh = 0;
+    for (int t = nq - 1; t >= 0 && fb < 0; --t) {  // wave-uniform
+#pragma unroll
+      for (int c = 0; c < kVlMaxSeqs / 64; ++c) {
+        const uint64_t m = __builtin_amdgcn_ballot_w64(nbk[c] > t);
+        const int64_t cnt = (int64_t)__builtin_popcountll(m) * p.H;
+        if (fb < 0) {
+          if (rem < cnt) {
+            const int k = (int)(rem / p.H);
+            const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            const uint64_t sel = __builtin_amdgcn_ballot_w64(((m >> lane) & 1u) != 0 && rank == k);
+            fb = c * 64 + __builtin_ctzll(sel);
+            ft = t;
+            fh = (int)(rem - (int64_t)k * p.H);
+          } else {
+            rem -= cnt;
+          }
+        }
+      }
+    }
+    if (fb < 0) return;  // past the last unit (work-group uniform)
+    qt = ft;
+    h = fh;
+    b = fb;
+  } else {
+    int64_t x = blockIdx.x;
+    if (p.wg_cus > 0) {
+      const int64_t C = p.wg_cus, g = x / C, j = x - g * C;
+      if ((g & 1) && (g + 1) * C <= nbh * nq) x = g * C + (C % 8 == 0 ? C - 8 - (j & ~(int64_t)7) + (j & 7) : C - 1 - j);
+    }
+    qt = nq - 1 - (int)(x / nbh);
+    const int64_t bh = x % nbh;
+    h = (int)(bh % p.H);
+    b = (int)(bh / p.H);
   }
-  const int qt = nq - 1 - (int)(x / nbh);
-  const int64_t bh = x % nbh;
-  const int h = (int)(bh % p.H);
-  const int b = (int)(bh / p.H);
   const int kvh = h / p.G;
 
   // This sequence's query rows: S of them (row r at position ctx - S + r)
@@ -1317,10 +1368,20 @@ static hipError_t launch_pf_q(const PrefillParams& p, hipStream_t stream) {
   PrefillParams q = p;
   constexpr int QB = kSplit ? 2 * PfShape<D>::QW : PfShape<D>::QB;
   q.q_tiles = (p.S + QB - 1) / QB;
-  const int64_t units = (int64_t)q.B * q.H * q.q_tiles;
+  int64_t units = (int64_t)q.B * q.H * q.q_tiles;
   int64_t cus = 0, per_cu = 0;
   residency(kernel, cache, &cus, &per_cu);
   q.wg_cus = units > cus && units <= cus * per_cu ? (int32_t)cus : 0;  // one resident wave
+  // Variable-length batches of up to kVlMaxSeqs sequences: a compacted grid
+  // of at most the units with rows (sum over sequences of ceil(rows / QB) <
+  // T / QB + sequences).
+  q.vl_compact = 0;
+  if (p.cu_q && p.B <= kVlMaxSeqs) {
+    const int64_t ub = (p.q_total + QB - 1) / QB + std::min<int64_t>(p.B, p.q_total);
+    units = (int64_t)q.H * std::min<int64_t>((int64_t)q.B * q.q_tiles, ub);
+    q.vl_compact = 1;
+    q.wg_cus = 0;
+  }
   note_launch("pa::prefill_mfma_kernel<%s, %d, %s, %s>", KV::kName, D, kSplitQ ? "true" : "false",
               kSplit ? "true" : "false");
   hipLaunchKernelGGL(kernel, dim3((unsigned)units), dim3(kPfThreads), 0, stream, q);

@@ -228,6 +228,33 @@ def test_varlen_mixed_decode_and_prefill(pa, dev, kv, D):
                                            inp["ctx"][b:b + 1], 1.0 / np.sqrt(D), kv))
 
 
+@pytest.mark.parametrize("B", [130, 300])
+def test_varlen_many_sequences(pa, dev, B):
+    """Many sequences of assorted lengths (0, 1, 2, 63, 64, 65, 129, 200 rows)
+    in one varlen call: up to 256 sequences the prefill grid holds only the
+    query blocks that have rows (numbered across chunks of 64 sequences),
+    beyond that every block of every sequence; every row against the oracle."""
+    rng = np.random.default_rng(B)
+    qlens = rng.choice([0, 1, 2, 63, 64, 65, 129, 200], size=B).tolist()
+    qlens[-1] = 200
+    ctxs = [int(n + rng.integers(0, 100)) for n in qlens]
+    inp, q, q32, cu = varlen_case(qlens, ctxs, 2, 2, 64, 16, seed=B, kv="f16", qt="f16")
+    T = int(cu[-1])
+    out = torch.full((max(T, 1), 2, 64), 7.0, device=dev)
+    pa.paged_attention_prefill_varlen(to_dev(q, "f16", dev), to_dev(inp["k"], "f16", dev),
+                                      to_dev(inp["v"], "f16", dev), torch.from_numpy(inp["bt"]).to(dev),
+                                      torch.from_numpy(inp["ctx"]).to(dev), torch.from_numpy(cu).to(dev),
+                                      max(qlens), 0.125, out=out)
+    got = to_host(out)
+    for b, n in enumerate(qlens):
+        if n == 0:
+            continue
+        rows = slice(cu[b], cu[b + 1])
+        want = oracle.prefill(q32[rows][None], inp["k"], inp["v"], inp["bt"][b:b + 1], inp["ctx"][b:b + 1],
+                              0.125, "f16")[0]
+        close(got[rows], want)
+
+
 def test_varlen_malformed_ranges_and_max_q_len(pa, dev):
     """A decreasing range and a range past T are skipped, rows past max_q_len
     are not written (sentinel kept), and the other sequences are unaffected."""
