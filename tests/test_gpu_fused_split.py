@@ -159,6 +159,38 @@ def test_fused_split_bad_block_id(pa, dev):
     close(got[keep], want)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_fused_split_fp8_scaled(pa, dev, D):
+    """An FP8 E4M3 cache with per-tensor scales (k_scale folded into the
+    softmax scale, v_scale applied to the merged output) through the fused
+    split, against the oracle on the dequantised cache and against a split
+    that runs as two launches."""
+    from test_gpu_decode import fp8_case, fp8_dev
+    H, BS, MB = 8, 16, 32
+    kvb = 1
+    lo = 2 if D * kvb < 128 else 1
+    B = grid_rows(dev, H, lo)
+    maxctx = MB * BS
+    rng = np.random.default_rng(D)
+    ctx = rng.integers(1, maxctx + 1, size=B).astype(np.int32)
+    ctx[:3] = [1, maxctx, 2]
+    inp, k8, v8, kf, vf = fp8_case(B, H, H, D, BS, ctx.tolist(), seed=D + 3, k_scale=0.05, v_scale=0.02)
+    bt = torch.from_numpy(inp["bt"]).to(dev)
+    cd = torch.from_numpy(inp["ctx"]).to(dev)
+    q = torch.from_numpy(inp["q_f32"]).to(dev).half()
+    k, v = fp8_dev(k8, dev), fp8_dev(v8, dev)
+    S = 64
+    assert expect_fused(pa, B, H, D, kvb, MB, BS, S, dev)
+    got = to_host(pa.paged_attention_v3(q, k, v, bt, cd, 0.1, S, k_scale=0.05, v_scale=0.02))
+    assert "reduce_kernel" not in pa.last_launch(), pa.last_launch()
+    q32 = oracle.to_float(oracle.quantize(inp["q_f32"], "f16"), "f16")
+    close(got, oracle.decode(q32, kf, vf, inp["bt"], inp["ctx"], 0.1, "f32"))
+    # Beside it, a split of five partitions (too few for the token slots: two launches).
+    got5 = to_host(pa.paged_attention_v3(q, k, v, bt, cd, 0.1, 5, k_scale=0.05, v_scale=0.02))
+    assert "reduce_kernel" in pa.last_launch(), pa.last_launch()
+    close(got, got5)
+
+
 def test_small_grid_keeps_two_launches(pa, dev):
     """A grid of one work-group per (row, head) that would not fill the GPU
     keeps the partition kernel and the reduce (both launched by one call)."""
