@@ -127,6 +127,8 @@ constexpr int kPfThreads = 256;   // 4 waves
 constexpr int kVlMaxSeqs = 256;   // variable-length batches numbered compactly (four per lane)
 constexpr int kPfBtStage = 1024;  // block-table entries staged in LDS
 constexpr float kLazyRescale = 8.0f;  // raise the running max only past 2^8
+constexpr float kWeightCap = 32768.0f;  // 8-wave kernel: raise it when a lane's weights sum past 2^15
+                                        // (weights up to 2^15 are exact in fp16 and bf16 range)
 
 
 // How a tile's P.V product is formed.
@@ -1098,18 +1100,53 @@ void prefill_pp_kernel(const PrefillParams p) {
           }
         }
       }
-      // Maximum over four independent chains (short dependency chains).
-      float mc[4];
+      // Weights against the running maximum m, packed as the P^T operands,
+      // and their row sum over the rounded weights (four chains, added at the
+      // end): each lane's sum over its 16 keys of the row.
+      auto weights = [&](float negm) __attribute__((always_inline)) {
+        float ls[MT][2];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        mc[c] = st[c >> 1][(c & 1) * 8];
+        for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-        for (int r = 1; r < 8; ++r) mc[c] = fmaxf(mc[c], st[c >> 1][(c & 1) * 8 + r]);
-      }
-      const float mx = fmaxf(fmaxf(mc[0], mc[1]), fmaxf(mc[2], mc[3]));
-      const float mxh = mx * qscale;
-      if (__builtin_amdgcn_ballot_w64(mxh > m + kLazyRescale) != 0) {
+          for (int s2 = 0; s2 < 2; ++s2) {
+            uint32_t w[4], wl[4];
+            float lc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float p0 = fast_exp2(fmaf(st[mt][8 * s2 + 2 * j], qscale, negm));
+              const float p1 = fast_exp2(fmaf(st[mt][8 * s2 + 2 * j + 1], qscale, negm));
+              w[j] = pack2<kPvBf16>(p0, p1);
+              if constexpr (kPvBf16) {
+                const float2_t r = unpack2<true>(w[j]);
+                wl[j] = pack2<true>(p0 - r[0], p1 - r[1]);
+                lc += p0 + p1;
+              } else {
+                lc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w[j]), half2_t{1.0f16, 1.0f16}, lc, false);
+              }
+            }
+            ls[mt][s2] = lc;
+            pb[mt][s2] = u32x4_t{w[0], w[1], w[2], w[3]};
+            if constexpr (kPvBf16) pb_lo[mt][s2] = u32x4_t{wl[0], wl[1], wl[2], wl[3]};
+          }
+        }
+        return (ls[0][0] + ls[0][1]) + (ls[1][0] + ls[1][1]);
+      };
+      // The maximum is raised only when needed: on the first tile (every
+      // live row sees key 0), or when a lane's weights could leave the range
+      // they are exact in (a sum above 2^15, or not finite: a weight past
+      // 2^15).  The tile maximum is computed only then.
+      float lsum = weights(m == -__builtin_inff() ? 0.0f : -m);
+      if (__builtin_amdgcn_ballot_w64(t == 0 || !(lsum <= kWeightCap)) != 0) {
         asm volatile("");
+        // Maximum over four independent chains (short dependency chains).
+        float mc[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          mc[c] = st[c >> 1][(c & 1) * 8];
+#pragma unroll
+          for (int r = 1; r < 8; ++r) mc[c] = fmaxf(mc[c], st[c >> 1][(c & 1) * 8 + r]);
+        }
+        const float mxh = fmaxf(fmaxf(mc[0], mc[1]), fmaxf(mc[2], mc[3])) * qscale;
         const float mxs = fmaxf(mxh, __shfl_xor(mxh, 32, 64));
         const float mn = fmaxf(m, mxs);
         const float corr = mn == -__builtin_inff() ? 1.0f : fast_exp2(m - mn);
@@ -1117,35 +1154,9 @@ void prefill_pp_kernel(const PrefillParams p) {
         l *= corr;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;
+        lsum = weights(m == -__builtin_inff() ? 0.0f : -m);
       }
-      const float negm = m == -__builtin_inff() ? 0.0f : -m;
-      // The row sum over the rounded weights in four chains, added at the end.
-      float ls[MT][2];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          uint32_t w[4], wl[4];
-          float lc = 0.0f;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float p0 = fast_exp2(fmaf(st[mt][8 * s2 + 2 * j], qscale, negm));
-            const float p1 = fast_exp2(fmaf(st[mt][8 * s2 + 2 * j + 1], qscale, negm));
-            w[j] = pack2<kPvBf16>(p0, p1);
-            if constexpr (kPvBf16) {
-              const float2_t r = unpack2<true>(w[j]);
-              wl[j] = pack2<true>(p0 - r[0], p1 - r[1]);
-              lc += p0 + p1;
-            } else {
-              lc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w[j]), half2_t{1.0f16, 1.0f16}, lc, false);
-            }
-          }
-          ls[mt][s2] = lc;
-          pb[mt][s2] = u32x4_t{w[0], w[1], w[2], w[3]};
-          if constexpr (kPvBf16) pb_lo[mt][s2] = u32x4_t{wl[0], wl[1], wl[2], wl[3]};
-        }
-      }
-      l += (ls[0][0] + ls[0][1]) + (ls[1][0] + ls[1][1]);
+      l += lsum;
     };
     // Matrix step: O^T += V^T . P^T of tile j - 1 (V in slot SV), then
     // S^T = K . Q^T of tile j (K in slot SK).  Each LDS operand is read two
