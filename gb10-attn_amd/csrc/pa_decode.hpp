@@ -829,64 +829,63 @@ void decode_kernel(const DecodeParams p) {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[0][e] = aT[e];
   } else {
-  const bool fast = (p.BS % TPI) == 0 && (t0 % TPI) == 0;
-  if (T0 < T1) {
-    const int pg0 = (int)fastdiv((uint32_t)T0, p.bs_div);
-    const int pg1 = (int)fastdiv((uint32_t)(T1 - 1), p.bs_div) + 1;
-    for (int cp = pg0; cp < pg1; cp += kBtChunk) {
-      const int np = min(kBtChunk, pg1 - cp);
-      __syncthreads();
-      if (bt_early && cp == pg0 && pg0 == pg_early) {
-        static_assert(kBtChunk <= kDecodeThreads, "one prefetched entry per thread");
-        if ((int)threadIdx.x < np) s_bt[threadIdx.x] = bt_pre;
-      } else {
-        for (int i = threadIdx.x; i < np; i += kDecodeThreads) s_bt[i] = bt_row[cp + i];
-      }
-      __syncthreads();
-      const int ct0 = max(t0, cp * p.BS);
-      const int ct1 = min(t1, (cp + np) * p.BS);
-      // Two tiles per wave in flight: the loads of the next tile are issued
-      // before the current one is consumed.  The next-tile issue is
-      // unconditional (past the end it reads the masked safe row), so every
-      // path reaching a consume has the same loads outstanding and the wait
-      // before it covers only the current tile.
-      auto sweep = [&](auto&& iss) {
-        const int kStep = wpm ? TT : NW * TT;  // this wave's tiles: its own partition's, or every NW-th
-        const int first = wpm ? ct0 : ct0 + wave * TT;
-        if (first < ct1) {
-          // Counted, branch-free body: tile j+1 is issued before tile j is
-          // consumed.  Every entry of the loop header has exactly one tile
-          // (in A) outstanding, so the waits stay partial.
-          const int ntw = (ct1 - first + kStep - 1) / kStep;  // tiles of this wave
-          Tile A, B;
-          int tile = first;
-          const bool prio = PPRIO && p.pprio;  // work-group uniform
-          if (prio) __builtin_amdgcn_s_setprio(3);
-          const int e1 = (ntw / 2) & ~1, e2 = (3 * ntw / 4) & ~1, e3 = (7 * ntw / 8) & ~1;
-          iss(tile, cp, ct1, A);
-          for (int j = 0; j + 1 < ntw; j += 2) {
-            if (prio) {
-              if (j == e1) __builtin_amdgcn_s_setprio(2);
-              if (j == e2) __builtin_amdgcn_s_setprio(1);
-              if (j == e3) __builtin_amdgcn_s_setprio(0);
-            }
-            iss(tile + kStep, cp, ct1, B);
-            consume(A);
-            iss(tile + 2 * kStep, cp, ct1, A);
-            consume(B);
-            tile += 2 * kStep;
-          }
-          if (ntw & 1) consume(A);
+    const bool fast = (p.BS % TPI) == 0 && (t0 % TPI) == 0;
+    if (T0 < T1) {
+      const int pg0 = (int)fastdiv((uint32_t)T0, p.bs_div);
+      const int pg1 = (int)fastdiv((uint32_t)(T1 - 1), p.bs_div) + 1;
+      for (int cp = pg0; cp < pg1; cp += kBtChunk) {
+        const int np = min(kBtChunk, pg1 - cp);
+        __syncthreads();
+        if (bt_early && cp == pg0 && pg0 == pg_early) {
+          static_assert(kBtChunk <= kDecodeThreads, "one prefetched entry per thread");
+          if ((int)threadIdx.x < np) s_bt[threadIdx.x] = bt_pre;
+        } else {
+          for (int i = threadIdx.x; i < np; i += kDecodeThreads) s_bt[i] = bt_row[cp + i];
         }
-      };
-      if (fast) {
-        sweep(issue_fast);
-      } else {
-        sweep(issue);
+        __syncthreads();
+        const int ct0 = max(t0, cp * p.BS);
+        const int ct1 = min(t1, (cp + np) * p.BS);
+        // Two tiles per wave in flight: the loads of the next tile are issued
+        // before the current one is consumed.  The next-tile issue is
+        // unconditional (past the end it reads the masked safe row), so every
+        // path reaching a consume has the same loads outstanding and the wait
+        // before it covers only the current tile.
+        auto sweep = [&](auto&& iss) {
+          const int kStep = wpm ? TT : NW * TT;  // this wave's tiles: its own partition's, or every NW-th
+          const int first = wpm ? ct0 : ct0 + wave * TT;
+          if (first < ct1) {
+            // Counted, branch-free body: tile j+1 is issued before tile j is
+            // consumed.  Every entry of the loop header has exactly one tile
+            // (in A) outstanding, so the waits stay partial.
+            const int ntw = (ct1 - first + kStep - 1) / kStep;  // tiles of this wave
+            Tile A, B;
+            int tile = first;
+            const bool prio = PPRIO && p.pprio;  // work-group uniform
+            if (prio) __builtin_amdgcn_s_setprio(3);
+            const int e1 = (ntw / 2) & ~1, e2 = (3 * ntw / 4) & ~1, e3 = (7 * ntw / 8) & ~1;
+            iss(tile, cp, ct1, A);
+            for (int j = 0; j + 1 < ntw; j += 2) {
+              if (prio) {
+                if (j == e1) __builtin_amdgcn_s_setprio(2);
+                if (j == e2) __builtin_amdgcn_s_setprio(1);
+                if (j == e3) __builtin_amdgcn_s_setprio(0);
+              }
+              iss(tile + kStep, cp, ct1, B);
+              consume(A);
+              iss(tile + 2 * kStep, cp, ct1, A);
+              consume(B);
+              tile += 2 * kStep;
+            }
+            if (ntw & 1) consume(A);
+          }
+        };
+        if (fast) {
+          sweep(issue_fast);
+        } else {
+          sweep(issue);
+        }
       }
     }
-  }
-
   }  // slot-partition mode / plain sweep
   rebase();
   combine_slots();
