@@ -353,9 +353,11 @@ int make_plan(const DecodeParams& p, int gc, int kv_bytes, int64_t num_splits, P
   const int lo = decode_pack_min(p.D, kv_bytes, p.G, p.HKV, p.k_sh);
   const int hi = decode_pack_max(p.D, kv_bytes, p.G, p.HKV, p.k_sh);
   const int64_t maxctx = (int64_t)p.MB * p.BS;
+  // (A unit of c packed heads streams c * D elements per token: its head
+  // dimension for the planner's stream-length rule.)
   auto parts_for = [&](int c, int64_t* ptok) {
     int64_t np = 0;
-    pa_plan_partitions(p.B, (p.HKV / c) * p.G, p.HKV / c, p.D, maxctx, cus, ptok, &np);
+    pa_plan_partitions(p.B, (p.HKV / c) * p.G, p.HKV / c, (int64_t)p.D * c, maxctx, cus, ptok, &np);
     return np;
   };
   int64_t ptok = 0;
