@@ -108,3 +108,44 @@ def test_noalloc_graph_capture_and_replay(pa, dev):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, ref), i
+
+
+def test_noalloc_fused_explicit_split_and_graph(pa, dev):
+    """The reference's split count over an MHA grid that fills the GPU runs
+    fused (one launch, the partials kept in registers, the fixed scratch not
+    written): the allocation-free entry equals the workspace entry bit for
+    bit, eagerly and recorded into a HIP graph replayed on changed q and
+    context lengths."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    H, D, BS, MB, ns = 8, 64, 16, 64, 64
+    B = -(-cus // H)
+    rng = np.random.default_rng(5)
+    ctxs = rng.integers(1, MB * BS + 1, size=B).tolist()
+    inp = decode_case(B, H, H, D, BS, ctxs, seed=51, kv="f16", q="f16", mb=MB)
+    q, k, v, bt, ctx = dev_inputs(inp, dev)
+    scale = 1.0 / np.sqrt(D)
+    out = torch.empty_like(q)
+    ref = torch.empty_like(q)
+    print(f"noalloc fused case B={B} H={H} D={D} splits={ns}", flush=True)
+    assert _noalloc(pa, out, q, k, v, bt, ctx, scale, ns) == 0, pa.last_error()
+    assert pa.last_launch() == "pa::decode_kernel<pa::KvF16, 64, 1, 1, 1>", pa.last_launch()
+    _with_workspace(pa, ref, q, k, v, bt, ctx, scale, ns)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    close(to_host(out), oracle.decode(inp["q_f32"], inp["k"], inp["v"], inp["bt"], inp["ctx"], scale, "f16"))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = _noalloc(pa, out, q, k, v, bt, ctx, scale, ns)
+    assert rc == 0, pa.last_error()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(52)
+    for i in range(3):
+        print(f"noalloc fused graph replay {i}", flush=True)
+        q.copy_(torch.randn(q.shape, generator=gen, device=dev).to(q.dtype))
+        ctx.copy_(torch.randint(0, MB * BS + 1, ctx.shape, generator=gen, device=dev).to(ctx.dtype))
+        _with_workspace(pa, ref, q, k, v, bt, ctx, scale, ns)
+        out.fill_(7.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), i
