@@ -255,6 +255,35 @@ def test_varlen_many_sequences(pa, dev, B):
         close(got[rows], want)
 
 
+@pytest.mark.parametrize("kv", ["f16", "bf16"])
+def test_varlen_on_the_8_wave_kernel(pa, dev, kv):
+    """A varlen batch whose rows fill the GPU twice over in 256-row blocks
+    (H x ceil(T / 256) >= 2 x CUs) runs on the 8-wave kernel: decode rows
+    (served by the decode kernel), an empty sequence, chunks of 1, 255, 256,
+    257 and 700 rows against longer contexts; every row against the oracle."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    qlens = [1, 255, 0, 256, 1, 257, 700, 2]
+    ctxs = [900, 300, 50, 256, 17, 400, 1000, 2]
+    T = sum(qlens)
+    H = 8 * -(-2 * cus // (8 * -(-T // 256)))  # H x ceil(T / 256) >= 2 x CUs
+    HKV = H // 4
+    D = 64
+    inp, q, q32, cu = varlen_case(qlens, ctxs, H, HKV, D, 16, seed=H + (kv == "bf16"), kv=kv, qt=kv)
+    got = to_host(pa.paged_attention_prefill_varlen(
+        to_dev(q, kv, dev), to_dev(inp["k"], kv, dev), to_dev(inp["v"], kv, dev),
+        torch.from_numpy(inp["bt"]).to(dev), torch.from_numpy(inp["ctx"]).to(dev),
+        torch.from_numpy(cu).to(dev), max(qlens), 0.125))
+    launched = pa.last_launch()
+    assert "prefill_pp_kernel" in launched and "decode_kernel" in launched, launched
+    for b, n in enumerate(qlens):
+        if n == 0:
+            continue
+        rows = slice(cu[b], cu[b + 1])
+        want = oracle.prefill(q32[rows][None], inp["k"], inp["v"], inp["bt"][b:b + 1], inp["ctx"][b:b + 1],
+                              0.125, kv)[0]
+        close(got[rows], want)
+
+
 def test_varlen_malformed_ranges_and_max_q_len(pa, dev):
     """A decreasing range and a range past T are skipped, rows past max_q_len
     are not written (sentinel kept), and the other sequences are unaffected."""
