@@ -172,6 +172,9 @@ int scratch_address(void** ptr) {
 // Longest explicit partition (tokens, at the block table's capacity) served
 // in the wave-partition mode.
 constexpr int64_t kWavePartTokens = 256;
+// Shortest explicit partition (tokens, at the block table's capacity) whose
+// split dispatches its sequences longest first.
+constexpr int64_t kLongestFirstTokens = 1024;
 
 struct PlanKnobs {
   int64_t wgs_per_cu = 3;
@@ -491,6 +494,14 @@ int run_v3(pa_tensor_t* out, const pa_tensor_t* q, const pa_tensor_t* k, const p
     if ((rc = device_cu_count(&cus))) return rc;
     a.p.hp = pack_for(a.p, dtype_bytes(a.kv_dtype), plan.parts, cus);
   }
+  // An explicit split into long partitions over up to 64 sequences orders
+  // the sequences longest first (the kernel ranks the context lengths; one
+  // more memory round trip per work-group, which short partitions do not
+  // repay): config 3's ragged batch at 8 splits (partitions up to 4096
+  // tokens) 5.33 -> 6.17 TB/s; at 64 splits (up to 512) -2 %, and config 2's
+  // uniform batch at 8 or 64 splits -3.7 %, hence the bound.
+  a.p.seq_order = num_splits > 0 && !plan.direct && a.p.B <= 64 && a.p.Sq == 1 &&
+                  (maxctx + plan.parts - 1) / plan.parts >= kLongestFirstTokens ? 1 : 0;
   if (!plan.direct) bind_workspace(&a.p, ws, plan);
   hipStream_t s = static_cast<hipStream_t>(stream);
   t_decode_fused = 0;

@@ -66,6 +66,8 @@ struct DecodeParams {
   int32_t rounds;       // slot-partition mode: partitions each token slot serves in turn
   int32_t fuse_final;   // host: the call wants the output too and decode_fuse_rounds() allows it;
                         // kernel: the work-group covers every partition of its unit and writes it
+  int32_t seq_order;    // explicit split into long partitions, B <= 64, Sq = 1: sequences dispatched
+                        // longest first
   FastDiv bs_div;
   float qscale;         // scale * k_scale * log2(e): scores come out in log2 units
   float vscale;         // v_scale (FP8 caches): applied to the weighted V sum

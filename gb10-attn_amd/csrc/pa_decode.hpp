@@ -87,6 +87,23 @@ __device__ inline bool compact_unit(const DecodeParams& p, int id, int lane, int
   return true;
 }
 
+// Explicit splits into long partitions (DecodeParams::seq_order, set by the
+// host): the sequences' work-groups are dispatched in order of context
+// length, longest first (a sequence's partitions are all about equally
+// long), so a ragged batch's launch ends on its shortest partitions instead
+// of wherever a long sequence falls in the batch.  Rank r -> sequence (up to
+// 64 single-row sequences).
+__device__ inline int longest_first_seq(const DecodeParams& p, int r, int lane) {
+  const int c = lane < p.B ? p.context_lens[lane] : -1;
+  int rank = 0;
+  for (int j = 0; j < p.B; ++j) {  // wave-uniform bound
+    const int cj = __builtin_amdgcn_readlane(c, j);
+    rank += (cj > c || (cj == c && j < lane)) ? 1 : 0;
+  }
+  const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < p.B && rank == r);
+  return hit ? __builtin_ctzll(hit) : r;
+}
+
 template <typename KV, int D, int NIO = 0>
 struct DecodeShape {
   static constexpr int VEC = KV::kVec;         // elements per lane per load
@@ -204,6 +221,7 @@ void decode_kernel(const DecodeParams p) {
     part = id % p.parts;
     z = id / p.parts;
   }
+  if (p.seq_order) z = longest_first_seq(p, z, lane);  // work-group uniform
   // One head per work-group (MHA, unpacked): rotate the head order by the
   // (sequence, partition) index.  Work-groups reach the 8 XCDs round robin,
   // so without it an XCD keeps reading the same few 128-byte head slices of

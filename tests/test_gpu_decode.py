@@ -691,3 +691,46 @@ def test_compacted_grid_ragged_split(pa, dev, kv, H, HKV, qt):
     assert np.all(np.isnan(got[1]))
     want = oracle.decode(inp["q_f32"], inp["k"], inp["v"], inp["bt"], ctx, 0.125, kv)
     close(got[2:], want[2:])
+
+
+@pytest.mark.parametrize("kv,H,HKV", [("f16", 8, 8), ("bf16", 16, 4)])
+def test_explicit_long_split_longest_first(pa, dev, kv, H, HKV):
+    """An explicit split into long partitions (at least 1024 tokens at the
+    table's capacity) over a ragged batch dispatches the sequences longest
+    first: every sequence still gets its own partitions (K = 0: each
+    partition's l is exactly its token count, bit for bit) and the combined
+    call matches the oracle, including an empty and an over-long context."""
+    import ctypes as C
+    ctx = [8192, 17, 3000, 0, 5000, 1, 8000, 4096, 2500]
+    B, D, BS, S = len(ctx), 64, 16, 4
+    inp = decode_case(B, H, HKV, D, BS, ctx, seed=61 + H, kv=kv, q=kv, mb=8192 // BS)
+    q, k, v, bt, cd = dev_inputs(inp, dev)
+    ctx_run = inp["ctx"].copy()
+    ctx_run[1] = 8192 + 1  # beyond the table: NaN row
+    cdr = torch.from_numpy(ctx_run).to(dev)
+    got = to_host(pa.paged_attention_v3(q, k, v, bt, cdr, 0.125, S, out_dtype=torch.float32))
+    want = oracle.decode(inp["q_f32"], inp["k"], inp["v"], inp["bt"], ctx_run, 0.125, kv)
+    assert np.all(np.isnan(got[1])) and np.all(got[3] == 0.0)
+    live = [b for b in range(B) if b not in (1, 3)]
+    close(got[live], want[live])
+    # Partition bounds through K = 0 (f32 data: l is exact).
+    inp32 = decode_case(B, H, HKV, D, BS, ctx, seed=62, kv="f32", mb=8192 // BS)
+    q32, _, v32, bt32, cd32 = dev_inputs(inp32, dev)
+    k0 = torch.zeros_like(v32)
+    out = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+    ws = torch.zeros(pa.workspace_size(q32, k0, bt32, S), dtype=torch.uint8, device=dev)
+    V = pa.view
+    pa.check(pa.lib().pa_v3_partition(C.byref(V(out)), C.byref(V(q32)), C.byref(V(k0)), C.byref(V(v32)),
+                                      C.byref(V(bt32)), C.byref(V(cd32)), 1.0, S, ws.data_ptr(),
+                                      ws.numel(), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    rows = B * H * S
+    up = lambda x: (x + 255) // 256 * 256
+    w = ws.cpu().numpy()
+    l = w[up(rows * D * 4) + up(rows * 4):][:rows * 4].view(np.float32).reshape(B, H, S)
+    for b in range(B):
+        if ctx[b] == 0:
+            continue
+        for s in range(S):
+            st, en = oracle.partition_bounds(ctx[b], S, s)
+            assert np.all(l[b, :, s] == max(0, en - st)), (b, s, l[b, :, s])
