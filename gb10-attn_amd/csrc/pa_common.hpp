@@ -160,8 +160,8 @@ inline int decode_tpi(int D, int HP, int kv_bytes) {
 
 // Fused explicit split: one work-group per (sequence, head group) serves all
 // `parts` partitions in rounds of kDecodeWaves * tpi (a partition per token
-// slot), writes each one's partials and merges them into the output itself,
-// with no reduce launch.  The rounds it takes, or 0 when there are fewer
+// slot), merges each one's partials into the output in registers (none are
+// written), with no reduce launch.  The rounds it takes, or 0 when there are fewer
 // partitions than slots, more rounds than kMaxSlotRounds, or the
 // work-group's pages would not fit one staged block-table chunk.
 inline int decode_fuse_rounds(int64_t parts, int MB, int BS, int tpi) {
