@@ -840,18 +840,20 @@ void prefill_mfma_kernel(const PrefillParams p) {
 //
 // Phase ph, group g: step e = ph - g; even e = matrix step e / 2, odd e =
 // vector step e / 2.  Tile j's K is read in phases 2j (group 0) and 2j + 1
-// (group 1), its V (by the P.V of step j + 1) in 2j + 2 and 2j + 3.  Loads:
-//  * K of tile j + 2: group 1, direct to LDS at the end of its matrix step j
-//    (phase 2j + 1) into the third K buffer (the other waves of the group may
-//    still be reading K of tile j), waited at the end of its vector step j
-//    (phase 2j + 2);
-//  * V of tile j: group 0 at the end of its matrix step j (phase 2j), into
-//    registers (bf16, converted to fp16) or direct to LDS, finished (converted,
-//    substituted rows zeroed) and waited in its vector step (phase 2j + 1).
-// Every load is waited in a vector step, which reads no tile from LDS, so
-// the compiler's wait for direct-to-LDS loads before a tile read falls on
-// loads that are already complete.  Per-row offset tables (three, tile t in
-// t % 3) are built by wave 0 in its vector step j for tile j + 3.
+// (group 1), its V (by the P.V of step j + 1) in 2j + 2 and 2j + 3.  Loads
+// (at D >= 64 every thread of both groups loads its share of every K and V
+// tile, so the two groups' vector steps carry the same work; at D = 32, one
+// 16-byte chunk per thread of a group, group 1 loads K and group 0 V):
+//  * in its vector step j (phase 2j + 1 + g) a thread issues its chunks of K
+//    of tile j + 2, direct to LDS, and of V of tile j + 1 (bf16: into
+//    registers; otherwise direct to LDS) -- both buffers were last read in
+//    phase 2j - 1;
+//  * at the end of its matrix step j + 1 (phase 2j + 2 + g) it waits for
+//    them and finishes its V chunks (bf16 converted to fp16 and stored,
+//    substituted rows zeroed), before the barrier ahead of their first read
+//    (phase 2j + 4).
+// Per-row offset tables (three, tile t in t % 3) are built by wave 0 in its
+// vector step j for tile j + 3.
 template <int N>
 struct Slot {  // a compile-time buffer index
   static constexpr int value = N;
@@ -881,7 +883,6 @@ void prefill_pp_kernel(const PrefillParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = wave >> 2;
-  const int w4 = wave & 3;
   const int n = lane & 31;
   const int hh = lane >> 5;
 
@@ -971,12 +972,18 @@ void prefill_pp_kernel(const PrefillParams p) {
   const uint32_t v_sbb = (uint32_t)(p.v_sb * EB), v_stb = (uint32_t)(p.v_st * EB);
   const uint64_t nb = (uint64_t)p.num_blocks;
 
-  // This thread's chunks of a tile within its group (the four-wave kernel's
-  // mapping with w4 for the wave).
-  int prow[CPT], ksrc[CPT], vsrc[CPT];
+  // This thread's chunks of a tile.  With two or more chunks per thread of a
+  // group (D >= 64), both groups load half of every K tile and half of every
+  // V tile (CH chunks of each per thread), so the two groups' vector steps
+  // carry the same work; at D = 32 (one chunk) group 1 loads K, group 0 V.
+  constexpr bool kHalves = CPT % 2 == 0;
+  constexpr int CH = kHalves ? CPT / 2 : CPT;
+  auto cpos = [&](int c) { return kHalves ? c * 8 + wave : c * 4 + (wave & 3); };  // 64-chunk group of chunk c
+  const bool do_k = kHalves || grp == 1, do_v = kHalves || grp == 0;  // wave-uniform
+  int prow[CH], ksrc[CH], vsrc[CH];
 #pragma unroll
-  for (int c = 0; c < CPT; ++c) {
-    const int pos = (c * 4 + w4) * 64 + lane;
+  for (int c = 0; c < CH; ++c) {
+    const int pos = cpos(c) * 64 + lane;
     prow[c] = pos / NCH;
     ksrc[c] = kpos<D>(prow[c], pos % NCH) * 8 * EB;
     vsrc[c] = vpos<D>(prow[c], pos % NCH) * 8 * EB;
@@ -1018,57 +1025,60 @@ void prefill_pp_kernel(const PrefillParams p) {
     m = -__builtin_inff();
     l = 0.0f;
 
-    u32x4_t vreg[kDirectV ? 1 : CPT];
+    u32x4_t vreg[kDirectV ? 1 : CH];
     uint32_t umask = 0;
 
-    // Group 1: K of tile t straight to LDS.
+    // This thread's K chunks of tile t straight to LDS.
     auto issue_k = [&](auto slot) {
+      if (!do_k) return;
       const u64x2_t* tb = s_off[decltype(slot)::value];
       uint16_t* dK = sK[decltype(slot)::value];
-      uint64_t e[CPT];  // the K halves of all table entries first: one LDS round trip
+      uint64_t e[CH];  // the K halves of the table entries first: one LDS round trip
 #pragma unroll
-      for (int c = 0; c < CPT; ++c) e[c] = reinterpret_cast<const uint64_t*>(tb + prow[c])[0];
+      for (int c = 0; c < CH; ++c) e[c] = reinterpret_cast<const uint64_t*>(tb + prow[c])[0];
 #pragma unroll
-      for (int c = 0; c < CPT; ++c)
-        lds_dma16_async(kbase + e[c] + ksrc[c], (lds_void_t*)(dK + (c * 4 + w4) * 512));
+      for (int c = 0; c < CH; ++c)
+        lds_dma16_async(kbase + e[c] + ksrc[c], (lds_void_t*)(dK + cpos(c) * 512));
     };
-    // Group 0: V of tile t (to LDS, or to registers for conversion).
+    // This thread's V chunks of tile t (to LDS, or to registers for conversion).
     auto issue_v = [&](auto slot) {
+      if (!do_v) return;
       const u64x2_t* tb = s_off[decltype(slot)::value];
       uint16_t* dV = sV[decltype(slot)::value];
       umask = 0;
-      uint64_t e[CPT];  // the V halves of all table entries first: one LDS round trip
+      uint64_t e[CH];  // the V halves of the table entries first: one LDS round trip
 #pragma unroll
-      for (int c = 0; c < CPT; ++c) e[c] = reinterpret_cast<const uint64_t*>(tb + prow[c])[1];
+      for (int c = 0; c < CH; ++c) e[c] = reinterpret_cast<const uint64_t*>(tb + prow[c])[1];
 #pragma unroll
-      for (int c = 0; c < CPT; ++c) {
+      for (int c = 0; c < CH; ++c) {
         const uint32_t use = (uint32_t)e[c] & 1u;
         umask |= use << c;
         const char* va = vbase + (e[c] - use) + vsrc[c];
         if constexpr (kDirectV) {
-          lds_dma16_async(va, (lds_void_t*)(dV + (c * 4 + w4) * 512));
+          lds_dma16_async(va, (lds_void_t*)(dV + cpos(c) * 512));
         } else {
           vreg[c] = *reinterpret_cast<const u32x4_t*>(va);
         }
       }
     };
-    // Group 0, after its V loads are complete: zero substituted rows, or
+    // After this thread's V loads are complete: zero substituted rows, or
     // convert the staged bf16 V to fp16 (exact for 2^-17 <= |v| < 65504).
     auto finish_v = [&](auto slot) {
+      if (!do_v) return;
       uint16_t* dV = sV[decltype(slot)::value];
       if constexpr (kDirectV) {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads are not tracked by the compiler
-        if (umask != (1u << CPT) - 1u) {
+        if (umask != (1u << CH) - 1u) {
 #pragma unroll
-          for (int c = 0; c < CPT; ++c) {
+          for (int c = 0; c < CH; ++c) {
             if (!((umask >> c) & 1u))
-              *reinterpret_cast<u32x4_t*>(dV + ((c * 4 + w4) * 64 + lane) * 8) = u32x4_t{0u, 0u, 0u, 0u};
+              *reinterpret_cast<u32x4_t*>(dV + (cpos(c) * 64 + lane) * 8) = u32x4_t{0u, 0u, 0u, 0u};
           }
         }
       } else {
-        const bool all_used = __builtin_amdgcn_ballot_w64(umask != (1u << CPT) - 1u) == 0;
+        const bool all_used = __builtin_amdgcn_ballot_w64(umask != (1u << CH) - 1u) == 0;
 #pragma unroll
-        for (int c = 0; c < CPT; ++c) {
+        for (int c = 0; c < CH; ++c) {
           u32x4_t w;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
@@ -1079,7 +1089,7 @@ void prefill_pp_kernel(const PrefillParams p) {
             asm volatile("");
             if (!((umask >> c) & 1u)) w = u32x4_t{0u, 0u, 0u, 0u};
           }
-          *reinterpret_cast<u32x4_t*>(dV + ((c * 4 + w4) * 64 + lane) * 8) = w;
+          *reinterpret_cast<u32x4_t*>(dV + (cpos(c) * 64 + lane) * 8) = w;
         }
       }
     };
@@ -1231,10 +1241,9 @@ void prefill_pp_kernel(const PrefillParams p) {
       if (ntiles > 2) build(Slot<2>{}, 2);
     }
     __syncthreads();
-    if (grp == 1) {
-      if (ntiles > 0) issue_k(Slot<0>{});
+    if (ntiles > 0) {
+      issue_k(Slot<0>{});
       if (ntiles > 1) issue_k(Slot<1>{});
-    } else if (ntiles > 0) {
       issue_v(Slot<0>{});
       finish_v(Slot<0>{});
     }
@@ -1254,18 +1263,13 @@ void prefill_pp_kernel(const PrefillParams p) {
       // Matrix step j.
       mstep(Slot<B0>{}, Slot<B2>{}, j >= 1 && (j - 1) * KB < wave_kend, j < ntiles && j * KB < wave_kend);
       __builtin_amdgcn_sched_barrier(0);
-      if (grp == 0) {
-        if (j >= 1 && j < ntiles) finish_v(Slot<B0>{});  // V of tile j, loaded since vector step j - 1
-      } else if (j + 1 < ntiles) {
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // K of tile j + 1, loaded since vector step j - 1
-      }
+      // This thread's loads of vector step j - 1: V of tile j and K of tile j + 1.
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads are not tracked by the compiler
+      if (j >= 1 && j < ntiles) finish_v(Slot<B0>{});
       __syncthreads();
       // Vector step j.
-      if (grp == 0) {
-        if (j + 1 < ntiles) issue_v(Slot<B1>{});
-      } else if (j + 2 < ntiles) {
-        issue_k(Slot<B2>{});
-      }
+      if (j + 1 < ntiles) issue_v(Slot<B1>{});
+      if (j + 2 < ntiles) issue_k(Slot<B2>{});
       if (j < ntiles && j * KB < wave_kend) softmax(j);
       if (wave == 0 && j + 3 < ntiles) build(Slot<B0>{}, j + 3);
       __syncthreads();
