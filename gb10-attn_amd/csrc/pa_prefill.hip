@@ -827,7 +827,8 @@ void prefill_mfma_kernel(const PrefillParams p) {
   }
 }
 
-// Ping-pong prefill (64-key tiles, 16-bit caches, q in the KV type).  A
+// Ping-pong prefill (64-key tiles; 16-bit caches with q in the KV type, or
+// FP8 caches with fp16 or bf16 q, the codes staged in registers).  A
 // work-group of 8 waves serves 256 query rows (wave w owns rows 32w ..) and
 // is the only one on its CU, so each SIMD holds wave s of group 0 (waves 0-3)
 // and wave s + 4 of group 1.  Every phase ends at a work-group barrier, and
@@ -869,9 +870,10 @@ void prefill_pp_kernel(const PrefillParams p) {
   static_assert(Sh::KB == 64 && Sh::MT == 2, "64-key tiles");
   constexpr int QW = 32, QB = kPpRows, KB = 64, MT = 2, KS = Sh::KS, DT = Sh::DT, NCH = Sh::NCH;
   constexpr int CPT = Sh::CPT;  // chunks per thread of one group (256 threads) per tile
-  constexpr bool kBf16 = KV::kCode == kBF16;
-  constexpr int EB = 2;
-  static_assert(KV::kBytes == 2, "16-bit caches");
+  constexpr bool kBf16 = QkBf16<KV>::value;  // Q.K^T operand type
+  constexpr bool kF8 = KV::kCode == kFP8;    // tiles converted from FP8 codes; P.V in fp16
+  constexpr int EB = KV::kBytes;
+  static_assert(EB == 2 || kF8, "16-bit or FP8 caches");
 
   __shared__ __attribute__((aligned(16))) uint16_t sK[3][KB * D];
   __shared__ __attribute__((aligned(16))) uint16_t sV[3][KB * D];
@@ -1014,7 +1016,7 @@ void prefill_pp_kernel(const PrefillParams p) {
 
   auto run = [&](auto mode_tag) -> bool {
     constexpr int kMode = decltype(mode_tag)::value;
-    constexpr bool kDirectV = kMode != kPvConvert;
+    constexpr bool kDirectV = kMode != kPvConvert && kMode != kPvF8;
     constexpr bool kPvBf16 = kMode == kPvSplit;
 
 #pragma unroll
@@ -1025,11 +1027,13 @@ void prefill_pp_kernel(const PrefillParams p) {
     m = -__builtin_inff();
     l = 0.0f;
 
-    u32x4_t vreg[kDirectV ? 1 : CH];
+    u32x4_t vreg[kDirectV || kF8 ? 1 : CH];
+    u32x2_t kreg8[kF8 ? CH : 1], vreg8[kF8 ? CH : 1];  // FP8 codes of this thread's chunks
     uint32_t umask = 0;
 
-    // This thread's K chunks of tile t straight to LDS.
-    auto issue_k = [&](auto slot) {
+    // This thread's K chunks of tile t: straight to LDS, or (FP8) codes into
+    // registers `kr`.
+    auto issue_k = [&](auto slot, u32x2_t (&kr)[kF8 ? CH : 1]) {
       if (!do_k) return;
       const u64x2_t* tb = s_off[decltype(slot)::value];
       uint16_t* dK = sK[decltype(slot)::value];
@@ -1037,8 +1041,37 @@ void prefill_pp_kernel(const PrefillParams p) {
 #pragma unroll
       for (int c = 0; c < CH; ++c) e[c] = reinterpret_cast<const uint64_t*>(tb + prow[c])[0];
 #pragma unroll
-      for (int c = 0; c < CH; ++c)
-        lds_dma16_async(kbase + e[c] + ksrc[c], (lds_void_t*)(dK + cpos(c) * 512));
+      for (int c = 0; c < CH; ++c) {
+        if constexpr (kF8) {
+          kr[c] = *reinterpret_cast<const u32x2_t*>(kbase + e[c] + ksrc[c]);
+        } else {
+          lds_dma16_async(kbase + e[c] + ksrc[c], (lds_void_t*)(dK + cpos(c) * 512));
+        }
+      }
+    };
+    // FP8, after this thread's K loads of tile t are complete: codes -> Q.K^T
+    // type pairs (exact for every code; rows past the keys need no zeroing:
+    // their scores are masked).
+    auto finish_k = [&](auto slot, const u32x2_t (&kr)[kF8 ? CH : 1]) {
+      if constexpr (kF8) {
+        if (!do_k) return;
+        uint16_t* dK = sK[decltype(slot)::value];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+          uint32_t w[4];
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            if constexpr (kBf16) {
+              w[2 * j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kr[c][j], 1.0f, false));
+              w[2 * j + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kr[c][j], 1.0f, true));
+            } else {
+              w[2 * j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(kr[c][j], 1.0f, false));
+              w[2 * j + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(kr[c][j], 1.0f, true));
+            }
+          }
+          *reinterpret_cast<u32x4_t*>(dK + (cpos(c) * 64 + lane) * 8) = u32x4_t{w[0], w[1], w[2], w[3]};
+        }
+      }
     };
     // This thread's V chunks of tile t (to LDS, or to registers for conversion).
     auto issue_v = [&](auto slot) {
@@ -1054,7 +1087,9 @@ void prefill_pp_kernel(const PrefillParams p) {
         const uint32_t use = (uint32_t)e[c] & 1u;
         umask |= use << c;
         const char* va = vbase + (e[c] - use) + vsrc[c];
-        if constexpr (kDirectV) {
+        if constexpr (kF8) {
+          vreg8[c] = *reinterpret_cast<const u32x2_t*>(va);
+        } else if constexpr (kDirectV) {
           lds_dma16_async(va, (lds_void_t*)(dV + cpos(c) * 512));
         } else {
           vreg[c] = *reinterpret_cast<const u32x4_t*>(va);
@@ -1062,11 +1097,27 @@ void prefill_pp_kernel(const PrefillParams p) {
       }
     };
     // After this thread's V loads are complete: zero substituted rows, or
-    // convert the staged bf16 V to fp16 (exact for 2^-17 <= |v| < 65504).
+    // convert the staged bf16 V to fp16 (exact for 2^-17 <= |v| < 65504), or
+    // the FP8 codes to fp16 (exact; substituted rows zeroed: their codes may
+    // be NaN).
     auto finish_v = [&](auto slot) {
       if (!do_v) return;
       uint16_t* dV = sV[decltype(slot)::value];
-      if constexpr (kDirectV) {
+      if constexpr (kF8) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+          uint32_t w[4];
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            w[2 * j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(vreg8[c][j], 1.0f, false));
+            w[2 * j + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(vreg8[c][j], 1.0f, true));
+          }
+          const bool used = (umask >> c) & 1u;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) w[j] = used ? w[j] : 0u;
+          *reinterpret_cast<u32x4_t*>(dV + (cpos(c) * 64 + lane) * 8) = u32x4_t{w[0], w[1], w[2], w[3]};
+        }
+      } else if constexpr (kDirectV) {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads are not tracked by the compiler
         if (umask != (1u << CH) - 1u) {
 #pragma unroll
@@ -1242,9 +1293,12 @@ void prefill_pp_kernel(const PrefillParams p) {
     }
     __syncthreads();
     if (ntiles > 0) {
-      issue_k(Slot<0>{});
-      if (ntiles > 1) issue_k(Slot<1>{});
+      u32x2_t kreg8b[kF8 ? CH : 1];
+      issue_k(Slot<0>{}, kreg8);
+      if (ntiles > 1) issue_k(Slot<1>{}, kreg8b);
       issue_v(Slot<0>{});
+      finish_k(Slot<0>{}, kreg8);
+      if (ntiles > 1) finish_k(Slot<1>{}, kreg8b);
       finish_v(Slot<0>{});
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -1265,11 +1319,12 @@ void prefill_pp_kernel(const PrefillParams p) {
       __builtin_amdgcn_sched_barrier(0);
       // This thread's loads of vector step j - 1: V of tile j and K of tile j + 1.
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads are not tracked by the compiler
+      if (j >= 1 && j + 1 < ntiles) finish_k(Slot<B1>{}, kreg8);
       if (j >= 1 && j < ntiles) finish_v(Slot<B0>{});
       __syncthreads();
       // Vector step j.
       if (j + 1 < ntiles) issue_v(Slot<B1>{});
-      if (j + 2 < ntiles) issue_k(Slot<B2>{});
+      if (j + 2 < ntiles) issue_k(Slot<B2>{}, kreg8);
       if (j < ntiles && j * KB < wave_kend) softmax(j);
       if (wave == 0 && j + 3 < ntiles) build(Slot<B0>{}, j + 3);
       __syncthreads();
@@ -1297,7 +1352,9 @@ void prefill_pp_kernel(const PrefillParams p) {
     return true;
   };
 
-  if constexpr (kBf16) {
+  if constexpr (kF8) {
+    run(PvTag<kPvF8>{});
+  } else if constexpr (KV::kCode == kBF16) {
     if (!run(PvTag<kPvConvert>{})) {
       badkey = 0x7fffffff;
       run(PvTag<kPvSplit>{});
@@ -1445,7 +1502,7 @@ static hipError_t launch_pf(const PrefillParams& p, hipStream_t stream) {
     // The 8-wave kernel (one work-group per CU) for grids of at least two
     // of its work-groups per CU; below that its 256-row blocks leave CUs
     // idle at the end of the launch (config 4a: 384 work-groups, -20 %).
-    if constexpr (KV::kCode == kF16 || KV::kCode == kBF16) {
+    if constexpr (KV::kCode == kF16 || KV::kCode == kBF16 || KV::kCode == kFP8) {
       const int64_t pp_units = busy(kPpRows);
       if (!p.q_split && p.MB <= kPfBtStage && cus > 0 && pp_units >= 2 * cus) return launch_pp<KV, D>(p, stream);
     }
