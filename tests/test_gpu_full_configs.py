@@ -15,7 +15,8 @@ and check what the oracle can afford there:
   * configs 4a / 4b (causal prefill): query rows against the oracle's decode
     of the row's prefix (a prefill row is the decode of its prefix, which
     tests/test_oracle.py pins) -- every row of 4a, and at 4b every 16th row
-    plus the rows on each side of every 128-row work-group boundary;
+    plus the rows on each side of every 128-row work-group boundary; 4b's
+    geometry also over a scaled FP8 E4M3 pool (bf16 q);
   * config 5 (layer 11 of a [12, 2, 131072, 16, 12, 64] fp16 pool, 77 GB,
     K base 35.4 G elements in): the layer read in place against a copy of
     it, bit for bit, and sampled sequences against the oracle;
@@ -176,6 +177,34 @@ def test_prefill_config_full(pa, dev, name):
     rs = [r for _ in range(B) for r in rows]
     qd = q.float().cpu().numpy()[bs, rs]                    # [N, H, D]
     want = oracle_decode_rows(qd, host_kv(k), host_kv(v), bt_np[bs], np.asarray(rs, np.int32) + 1, scale, kv_tag(dt))
+    close(got[bs, rs], want)
+
+
+def test_prefill_config4b_fp8_full(pa, dev):
+    """Config 4b's geometry over an FP8 E4M3 pool (bf16 q, k and v scales
+    1/16) on the 8-wave kernel, the codes staged in registers: the rows of the
+    4b check against the oracle on the dequantised pool."""
+    B, S, H, D, _, rows = PREFILL["4b"]
+    BS, ks, vs = 16, 1.0 / 16, 1.0 / 16
+    g = torch.Generator(device=dev)
+    g.manual_seed(44)
+    bt_np, nb = ragged_tables([S] * B, BS, 45)
+    k8 = (randn((nb, BS, H, D), g, dev, torch.float32) / ks).to(torch.float8_e4m3fn)
+    v8 = (randn((nb, BS, H, D), g, dev, torch.float32) / vs).to(torch.float8_e4m3fn)
+    q = randn((B, S, H, D), g, dev, torch.bfloat16)
+    bt = torch.from_numpy(bt_np).to(dev)
+    cl = torch.full((B,), S, dtype=torch.int32, device=dev)
+    scale = 1.0 / np.sqrt(D)
+    got = to_host(pa.paged_attention_prefill_wmma(q, k8, v8, bt, cl, scale, k_scale=ks, v_scale=vs,
+                                                  out_dtype=torch.float32))
+    assert pa.last_launch().startswith("pa::prefill_pp_kernel<pa::KvFP8QkBf16, 128>"), pa.last_launch()
+    assert np.isfinite(got).all()
+    kf = oracle.fp8_decode(k8.view(torch.uint8).cpu().numpy()) * np.float32(ks)
+    vf = oracle.fp8_decode(v8.view(torch.uint8).cpu().numpy()) * np.float32(vs)
+    bs = [b for b in range(B) for _ in rows]
+    rs = [r for _ in range(B) for r in rows]
+    qd = q.float().cpu().numpy()[bs, rs]
+    want = oracle_decode_rows(qd, kf, vf, bt_np[bs], np.asarray(rs, np.int32) + 1, scale, "f32")
     close(got[bs, rs], want)
 
 

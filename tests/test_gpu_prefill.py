@@ -284,6 +284,35 @@ def test_varlen_on_the_8_wave_kernel(pa, dev, kv):
         close(got[rows], want)
 
 
+@pytest.mark.parametrize("qt", ["f16", "bf16"])
+def test_varlen_fp8_on_the_8_wave_kernel(pa, dev, qt):
+    """The same varlen batch over a scaled FP8 E4M3 pool (q fp16 or bf16):
+    the chunks run on the 8-wave kernel with the codes staged in registers,
+    the decode rows on the FP8 decode kernel; every row against the oracle on
+    the dequantised cache."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    qlens = [1, 255, 0, 256, 1, 257, 700, 2]
+    ctxs = [900, 300, 50, 256, 17, 400, 1000, 2]
+    T = sum(qlens)
+    H = 8 * -(-2 * cus // (8 * -(-T // 256)))  # H x ceil(T / 256) >= 2 x CUs
+    HKV, D, ks, vs = H // 4, 64, 0.04, 0.03
+    inp, q, q32, cu = varlen_case(qlens, ctxs, H, HKV, D, 16, seed=H + 5, kv="f32", qt=qt)
+    k8, v8 = oracle.fp8_encode(inp["k"] / np.float32(ks)), oracle.fp8_encode(inp["v"] / np.float32(vs))
+    kf, vf = oracle.fp8_decode(k8) * np.float32(ks), oracle.fp8_decode(v8) * np.float32(vs)
+    got = to_host(pa.paged_attention_prefill_varlen(
+        to_dev(q, qt, dev), _fp8(k8, dev), _fp8(v8, dev), torch.from_numpy(inp["bt"]).to(dev),
+        torch.from_numpy(inp["ctx"]).to(dev), torch.from_numpy(cu).to(dev), max(qlens), 0.125,
+        k_scale=ks, v_scale=vs))
+    launched = pa.last_launch()
+    assert "prefill_pp_kernel<pa::KvFP8" in launched and "decode_kernel" in launched, launched
+    for b, n in enumerate(qlens):
+        if n == 0:
+            continue
+        rows = slice(cu[b], cu[b + 1])
+        want = oracle.prefill(q32[rows][None], kf, vf, inp["bt"][b:b + 1], inp["ctx"][b:b + 1], 0.125, "f32")[0]
+        close(got[rows], want)
+
+
 def test_varlen_malformed_ranges_and_max_q_len(pa, dev):
     """A decreasing range and a range past T are skipped, rows past max_q_len
     are not written (sentinel kept), and the other sequences are unaffected."""
