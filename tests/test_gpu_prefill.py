@@ -480,23 +480,25 @@ def _fp8(a, dev):
 
 @pytest.mark.parametrize("qt", ["f16", "bf16"])
 @pytest.mark.parametrize("D", [32, 64, 128])
-def test_mfma_prefill_pingpong_fp8(pa, dev, qt, D):
+@pytest.mark.parametrize("BS", [16, 5])
+def test_mfma_prefill_pingpong_fp8(pa, dev, qt, D, BS):
     """FP8 E4M3 pools on the 8-wave kernel (q in fp16 or bf16, grids of at
     least two work-groups per CU): the K and V codes are staged in registers
     and written to LDS as exact 16-bit tiles.  Chunked, plain and padded rows
     over GQA-4 heads with per-tensor scales and NaN codes in every slot no row
-    attends, checked on the first and last KV heads' query heads; then a page
-    of invalid block id (exactly the rows that attend it are NaN)."""
+    attends, on pages of 16 and of 5 tokens, checked on the first and last KV
+    heads' query heads; then a page of invalid block id (exactly the rows
+    that attend it are NaN)."""
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     H = 4 * (-(-cus // 16))  # 4 sequences x 2 blocks of 256 rows x H heads >= 2 x CUs
-    S, BS, G = 260, 16, 4
+    S, G = 260, 4
     ks, vs = 0.05, 0.02
     inp, k8, v8, kf, vf = fp8_prefill_case(4, S, H, H // G, D, BS, [600, 120, 260, 400], seed=D + 7, qt=qt,
                                            k_scale=ks, v_scale=vs, poison=True)
     scale = 1.0 / np.sqrt(D)
     groups = [0, H // G - 1]
     heads = np.r_[0:G, H - G:H]
-    print(f"pingpong fp8 q={qt} D={D} H={H}", flush=True)
+    print(f"pingpong fp8 q={qt} D={D} BS={BS} H={H}", flush=True)
     q, k, v = to_dev(inp["q"], qt, dev), _fp8(k8, dev), _fp8(v8, dev)
     ctx = torch.from_numpy(inp["ctx"]).to(dev)
 
@@ -512,7 +514,7 @@ def test_mfma_prefill_pingpong_fp8(pa, dev, qt, D):
     close(got, want(inp["bt"]))
 
     bt = inp["bt"].copy()
-    bt[0, 30] = 10 ** 6  # keys 480..495 of sequence 0: rows at positions >= 480 are NaN
+    bt[0, 480 // BS] = 10 ** 6  # the page of key 480 of sequence 0: rows at positions >= its first key are NaN
     got = to_host(pa.paged_attention_prefill_wmma(q, k, v, torch.from_numpy(bt).to(dev), ctx, scale,
                                                   k_scale=ks, v_scale=vs))[:, :, heads]
     w = want(bt)
