@@ -846,13 +846,13 @@ void prefill_mfma_kernel(const PrefillParams p) {
 // tile, so the two groups' vector steps carry the same work; at D = 32, one
 // 16-byte chunk per thread of a group, group 1 loads K and group 0 V):
 //  * in its vector step j (phase 2j + 1 + g) a thread issues its chunks of K
-//    of tile j + 2, direct to LDS, and of V of tile j + 1 (bf16: into
-//    registers; otherwise direct to LDS) -- both buffers were last read in
-//    phase 2j - 1;
+//    of tile j + 2 and of V of tile j + 1: direct to LDS, except a bf16 V
+//    tile and FP8 codes, which go to registers -- both buffers were last
+//    read in phase 2j - 1;
 //  * at the end of its matrix step j + 1 (phase 2j + 2 + g) it waits for
-//    them and finishes its V chunks (bf16 converted to fp16 and stored,
-//    substituted rows zeroed), before the barrier ahead of their first read
-//    (phase 2j + 4).
+//    them and finishes them (bf16 V converted to fp16, FP8 K and V codes to
+//    16-bit pairs, and stored; substituted V rows zeroed), before the
+//    barrier ahead of their first read (phase 2j + 4).
 // Per-row offset tables (three, tile t in t % 3) are built by wave 0 in its
 // vector step j for tile j + 3.
 template <int N>
