@@ -313,6 +313,39 @@ def test_varlen_fp8_on_the_8_wave_kernel(pa, dev, qt):
         close(got[rows], want)
 
 
+@pytest.mark.parametrize("scale", [-0.15, 0.0])
+@pytest.mark.parametrize("kv", ["f16", "bf16", "fp8"])
+def test_mfma_prefill_pingpong_scale_sign(pa, dev, scale, kv):
+    """A negative scale (its sign is folded into q exactly; the running max
+    follows the scaled scores) and a zero scale (uniform weights over the
+    visible keys) on the 8-wave kernel, over fp16, bf16 and FP8 (bf16 q)
+    pools: the first and last KV heads' query heads against the oracle."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    H = 4 * (-(-cus // 16))  # 4 sequences x 2 blocks of 256 rows x H heads >= 2 x CUs
+    S, BS, G, D = 260, 16, 4, 64
+    ctx = [600, 120, 260, 400]
+    groups = [0, H // G - 1]
+    heads = np.r_[0:G, H - G:H]
+    if kv == "fp8":
+        inp, k8, v8, kf, vf = fp8_prefill_case(4, S, H, H // G, D, BS, ctx, seed=91, qt="bf16", k_scale=0.05,
+                                               v_scale=0.02)
+        q, k, v = to_dev(inp["q"], "bf16", dev), _fp8(k8, dev), _fp8(v8, dev)
+        kw = dict(k_scale=0.05, v_scale=0.02)
+        kref, vref, tag = kf, vf, "f32"
+    else:
+        inp = prefill_case(4, S, H, H // G, D, BS, ctx, seed=92, kv=kv, qt=kv)
+        q, k, v = to_dev(inp["q"], kv, dev), to_dev(inp["k"], kv, dev), to_dev(inp["v"], kv, dev)
+        kw = {}
+        kref, vref, tag = inp["k"], inp["v"], kv
+    got = pa.paged_attention_prefill_wmma(q, k, v, torch.from_numpy(inp["bt"]).to(dev),
+                                          torch.from_numpy(inp["ctx"]).to(dev), scale, **kw)
+    assert pa.last_launch().startswith("pa::prefill_pp_kernel<"), pa.last_launch()
+    want = np.concatenate([oracle.prefill(inp["q_f32"][:, :, g * G:(g + 1) * G], kref[:, :, g:g + 1],
+                                          vref[:, :, g:g + 1], inp["bt"], inp["ctx"], scale, tag) for g in groups],
+                          axis=2)
+    close(to_host(got)[:, :, heads], want)
+
+
 def test_varlen_malformed_ranges_and_max_q_len(pa, dev):
     """A decreasing range and a range past T are skipped, rows past max_q_len
     are not written (sentinel kept), and the other sequences are unaffected."""
