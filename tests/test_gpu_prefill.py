@@ -346,6 +346,26 @@ def test_mfma_prefill_pingpong_scale_sign(pa, dev, scale, kv):
     close(to_host(got)[:, :, heads], want)
 
 
+@pytest.mark.parametrize("ot", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shift", [0, 1])
+def test_mfma_prefill_pingpong_output(pa, dev, ot, shift):
+    """The 8-wave kernel's epilogue: fp32, fp16 and bf16 outputs, at an
+    aligned base (4 dims per store) and one element off (per-element
+    stores), against the oracle on the first and last KV heads' query heads."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    H = 4 * (-(-cus // 16))  # 4 sequences x 2 blocks of 256 rows x H heads >= 2 x CUs
+    S, BS, G, D = 260, 16, 4, 64
+    inp = prefill_case(4, S, H, H // G, D, BS, [600, 120, 260, 400], seed=93 + shift, kv="bf16", qt="bf16")
+    q = to_dev(inp["q"], "bf16", dev)
+    buf = torch.full((q.numel() + shift,), float("nan"), dtype=ot, device=dev)
+    out = buf[shift:].view(q.shape)
+    pa.paged_attention_prefill_wmma(q, *dev_args(inp, dev)[1:], 0.125, out=out)
+    assert pa.last_launch().startswith("pa::prefill_pp_kernel<"), pa.last_launch()
+    groups = [0, H // G - 1]
+    heads = np.r_[0:G, H - G:H]
+    close(to_host(out)[:, :, heads], _want_head_groups(inp, 0.125, groups))
+
+
 def test_varlen_malformed_ranges_and_max_q_len(pa, dev):
     """A decreasing range and a range past T are skipped, rows past max_q_len
     are not written (sentinel kept), and the other sequences are unaffected."""
