@@ -366,6 +366,32 @@ def test_mfma_prefill_pingpong_output(pa, dev, ot, shift):
     close(to_host(out)[:, :, heads], _want_head_groups(inp, 0.125, groups))
 
 
+def test_mfma_prefill_pingpong_edge_contexts(pa, dev):
+    """Edge rows on the 8-wave kernel: an empty sequence (every row padded:
+    zeros), a context longer than the block table holds (rows at q_pos >= 0
+    NaN, padded rows zeros), a 5-token context under a 260-row prompt, and a
+    plain one; every row of the first and last KV heads' query heads against
+    the oracle, NaN positions exactly."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    H = 4 * (-(-cus // 16))  # 4 sequences x 2 blocks of 256 rows x H heads >= 2 x CUs
+    S, BS, G, D = 260, 16, 4, 64
+    inp = prefill_case(4, S, H, H // G, D, BS, [0, 300, 5, 260], seed=94, kv="f16", qt="f16")
+    ctx = inp["ctx"].copy()
+    ctx[1] = inp["bt"].shape[1] * BS + 1  # beyond the table
+    q, k, v, bt, _ = dev_args(inp, dev)
+    got = to_host(pa.paged_attention_prefill_wmma(q, k, v, bt, torch.from_numpy(ctx).to(dev), 0.125))
+    assert pa.last_launch().startswith("pa::prefill_pp_kernel<"), pa.last_launch()
+    heads = np.r_[0:G, H - G:H]
+    groups = [0, H // G - 1]
+    want = np.concatenate([oracle.prefill(inp["q_f32"][:, :, g * G:(g + 1) * G], inp["k"][:, :, g:g + 1],
+                                          inp["v"][:, :, g:g + 1], inp["bt"], ctx, 0.125, "f16") for g in groups],
+                          axis=2)
+    got = got[:, :, heads]
+    assert np.all(want[0] == 0.0) and np.isnan(want[1]).any() and not np.isnan(want[2:]).any()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    close(got, want)
+
+
 def test_varlen_malformed_ranges_and_max_q_len(pa, dev):
     """A decreasing range and a range past T are skipped, rows past max_q_len
     are not written (sentinel kept), and the other sequences are unaffected."""
